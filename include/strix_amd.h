@@ -1,0 +1,136 @@
+/* SPDX-License-Identifier: MIT
+ *
+ * libstrix_amd: C ABI of the MI355X (gfx950) quantized-GEMM hot path.
+ *
+ * The reference exposes this path only as torch ops registered in
+ * csrc/torch_ops.cpp (TORCH_LIBRARY(strix, m), lines 179-304). Each entry
+ * point below is the torch-free launch layer under one of those ops: plain
+ * device pointers, element strides, sizes and a hipStream_t passed as void*.
+ * The Python package libstrix_amd binds them with ctypes and registers the
+ * same torch.ops.strix.* schemas on top.
+ *
+ * Conventions
+ *   - Every function returns STRIX_OK (0) or an error code; the message of the
+ *     last error on the calling thread is strix_last_error(). Argument checks
+ *     run before any HIP call, so they work on a machine without a GPU.
+ *   - Launches are asynchronous on `stream`; nothing synchronizes the host.
+ *   - Strides ("ld*") are in elements of the pointed-to type; byte tensors
+ *     (int8 / e4m3 / packed int4) count bytes.
+ *   - Activation dtype codes: STRIX_BF16, STRIX_F16 (16-bit storage).
+ *   - Weights are never copied or converted per call.
+ */
+#ifndef STRIX_AMD_H
+#define STRIX_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define STRIX_ABI_VERSION 1
+
+enum {
+  STRIX_OK = 0,
+  STRIX_ERR_INVALID = 1, /* bad argument: shape, dtype, stride, alignment */
+  STRIX_ERR_DEVICE = 2,  /* no device / not gfx950 */
+  STRIX_ERR_LAUNCH = 3   /* the HIP launch itself failed */
+};
+
+enum {
+  STRIX_BF16 = 0,
+  STRIX_F16 = 1,
+  STRIX_F32 = 2,
+  STRIX_I32 = 3
+};
+
+enum { STRIX_ACT_SILU = 0, STRIX_ACT_GELU_TANH = 1 };
+
+const char* strix_last_error(void);
+int strix_abi_version(void);
+
+/* ------------------------------------------------------------------ quant
+ * int8 per-token: s[m] = max|x[m,:]|/127 (1 if 0), q = clamp(rint(x/s),-127,127).
+ * New for BASELINE config 1 (the reference quantizes per 128-group inside
+ * w8a8_wmma_gemm, csrc/gemm/w8a8_wmma_gemm.hip:456-548). */
+int strix_int8_quant_per_token(const void* x, int x_dtype, int64_t ldx, int8_t* q, int64_t ldq,
+                               float* s, int64_t M, int64_t K, void* stream);
+/* int8 per (row, 128-group), s [M, lds]: moe_act_quant_i8
+ * (csrc/torch_ops.cpp:217, csrc/moe/moe_gemm_w4a8.hip:282-316). */
+int strix_int8_quant_group128(const void* x, int x_dtype, int64_t ldx, int8_t* q, int64_t ldq,
+                              float* s, int64_t lds, int64_t M, int64_t K, void* stream);
+/* e4m3fn per (row, 128-group): s = max|x|/448 (1 if 0), q = e4m3_rne(x/s).
+ * Absent in the reference (its FP8 path is W8A16, python/strix_vllm/fp8.py:122-124);
+ * the input quant step of vLLM's Fp8BlockScaledMMLinearKernel that strix disables. */
+int strix_fp8_quant_group128(const void* x, int x_dtype, int64_t ldx, uint8_t* q, int64_t ldq,
+                             float* s, int64_t lds, int64_t M, int64_t K, void* stream);
+
+/* ------------------------------------------------------------------ 8-bit GEMMs
+ * FP8-block W8A8: out[M,N] = sum_kb sa[m,kb] sw[n/128,kb] (qa[m,kb] . qw[n,kb]).
+ * qa e4m3 [M, lda], sa fp32 [M, sa_ld], w e4m3 [N, ldw], sw fp32 [ceil(N/128), sw_ld].
+ * cfg -1 picks the tile by M; 0..6 pins one (tile sweeps, cf. fp8_wmma_gemm_cfg,
+ * csrc/torch_ops.cpp:253). Replaces fp8_wmma_gemm's dense FP8 role
+ * (csrc/gemm/fp8_wmma_gemm.hip:253-322) with native e4m3 MFMA. */
+int strix_fp8_w8a8_block_gemm(const uint8_t* qa, int64_t lda, const float* sa, int64_t sa_ld,
+                              const uint8_t* w, int64_t ldw, const float* sw, int64_t sw_ld,
+                              void* out, int64_t ldo, int out_dtype, int64_t M, int64_t N,
+                              int64_t K, int cfg, void* stream);
+/* INT8 per-token W8A8: out = bf16((float(qa.qw) * sa[m]) * sw[n]); out_dtype
+ * STRIX_I32 writes the raw int32 accumulator (the bit-exactness probe). The
+ * per-token sibling of w8a8_wmma_gemm (csrc/gemm/w8a8_wmma_gemm.hip:799-918). */
+int strix_w8a8_int8_gemm(const int8_t* qa, int64_t lda, const float* sa, const int8_t* w, int64_t ldw,
+                         const float* sw, void* out, int64_t ldo, int out_dtype, int64_t M, int64_t N,
+                         int64_t K, int cfg, void* stream);
+/* INT8 per-128-group activations x int8 weights (signed, or uint8b128 when
+ * w_excess128), group or per-channel weight scales sw[n*sw_ns + g*sw_gs]:
+ * the GEMM of w8a8_wmma_gemm (csrc/torch_ops.cpp:277, csrc/gemm/w8a8_wmma_gemm.hip:151-443). */
+int strix_w8a8_int8_group_gemm(const int8_t* qa, int64_t lda, const float* sa, int64_t sa_ld,
+                               const uint8_t* w, int64_t ldw, int w_excess128, const float* sw,
+                               int64_t sw_ns, int64_t sw_gs, void* out, int64_t ldo, int out_dtype,
+                               int64_t M, int64_t N, int64_t K, int cfg, void* stream);
+/* FP8-block W8A8 grouped expert GEMM over aligned sorted ids (the W8A8
+ * sibling of moe_gemm_fp8, csrc/torch_ops.cpp:225-228,
+ * csrc/moe/moe_gemm_w8a16.hip:444-579). Rows of qa are tokens (slot / top_k);
+ * silu_mul fuses act(gate)*up ([gate; up] weight rows, c gets N/2 columns);
+ * topk_weights (may be NULL) scales each output row. */
+int strix_moe_gemm_fp8_w8a8(void* c, int64_t ldc, int c_dtype, const uint8_t* qa, int64_t lda,
+                            const float* sa, int64_t sa_ld, const uint8_t* w, int64_t w_es, int64_t ldw,
+                            const float* sw, int64_t sw_es, int64_t sw_ns, const int32_t* sorted_ids,
+                            int64_t sorted_len, const int32_t* expert_ids, int64_t num_blocks,
+                            const int32_t* num_post, const float* topk_weights, int64_t num_slots,
+                            int64_t top_k, int64_t block_m, int silu_mul, int activation, int64_t N,
+                            int64_t K, void* stream);
+
+/* ------------------------------------------------------------------ MoE plumbing
+ * Router: softmax -> top-k -> optional renormalize (vLLM fused_topk, called at
+ * python/strix_vllm/moe.py:181-184). ids by logit value, ties to the lower id. */
+int strix_moe_route_topk(const void* logits, int logits_dtype, int64_t ldl, int64_t T, int64_t E,
+                         int64_t top_k, int renormalize, int32_t* topk_ids, float* topk_weights,
+                         int64_t ldo, void* stream);
+/* moe_align_block_size contract (tests/test_moe_gemm.py:9-31): slot ids
+ * grouped by expert (ascending, stable), each run padded to block_m with id
+ * num_slots; expert_ids per block (-1 past the end); num_post = padded total. */
+int64_t strix_moe_align_sorted_capacity(int64_t num_slots, int64_t E, int64_t block_m);
+int64_t strix_moe_align_workspace_bytes(int64_t num_slots, int64_t E);
+int strix_moe_align(const int32_t* topk_ids, int64_t num_slots, int64_t E, int64_t block_m,
+                    int32_t* sorted_ids, int64_t sorted_cap, int32_t* expert_ids, int64_t blocks_cap,
+                    int32_t* num_post, void* workspace, int64_t workspace_bytes, void* stream);
+/* moe_sum (python/strix_vllm/moe.py:328-330): out[t] = sum_j w[t,j] * y[t*k+j]
+ * (w NULL = unweighted), fp32 in slot order. */
+int strix_moe_sum(const void* y, int dtype, int64_t ldy, int64_t T, int64_t top_k, int64_t H,
+                  const float* weights, void* out, int64_t ldo, void* stream);
+
+/* ------------------------------------------------------------------ probes
+ * Fragment-layout probes (the reference's _wmma_bf16_tile,
+ * csrc/torch_ops.cpp:183, csrc/testing/wmma_layout_test.hip:12-36).
+ * kind 0: bf16 a,b [16,K] -> fp32 d [16,16]; 1: e4m3 -> fp32; 2: int8 -> int32.
+ * d = a . b^T through one wave's MFMA chain. */
+int strix_probe_mfma(int kind, const void* a, const void* b, void* d, int64_t K, void* stream);
+/* global_load_lds_dwordx4 placement: dst = src with its 64 16-byte chunks reversed. */
+int strix_probe_g2l(const uint8_t* src, uint8_t* dst, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* STRIX_AMD_H */

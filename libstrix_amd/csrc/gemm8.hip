@@ -1,0 +1,725 @@
+// SPDX-License-Identifier: MIT
+// 8-bit MFMA GEMMs for gfx950: FP8-block W8A8 (e4m3 x e4m3 16x16x128 MFMA,
+// fp32 fold per 128-K block), INT8 per-token W8A8 (i8 x i8 16x16x64 MFMA,
+// exact int32 accumulator) and INT8 per-128-group W8A8 (int32 partial per
+// group folded into fp32). Dense and MoE (grouped over aligned sorted ids).
+//
+// Math (reference: csrc/gemm/w8a8_wmma_gemm.hip:15-32 for the group fold,
+// csrc/moe/moe_gemm_w8a16.hip:76-404 for the grouped MoE contract):
+//   FP8 block   out[m,n] = sum_kb sa[m,kb] * sw[n/128,kb] * sum_{k in kb} qa[m,k] qw[n,k]
+//   I8 token    out[m,n] = bf16((float(sum_k qa[m,k] qw[n,k]) * sa[m]) * sw[n])
+//   I8 group    out[m,n] = sum_g float(sum_{k in g} qa qw) * (sw[n,g] * sa[m,g])
+//
+// Two kernel shapes:
+//   stream8: no LDS staging. A wave owns NT 16-row weight subtiles and MT
+//            16-token subtiles; the waves of a block split K and reduce
+//            through LDS. Weights are streamed from HBM exactly once, 16 rows
+//            x 64 contiguous bytes per load instruction. Decode (M <= 64) and
+//            MoE blocks of 16-64 sorted ids.
+//   tiled8:  BM x BN block tile, direct global->LDS copies (no register
+//            staging) into a fragment-native layout, two LDS stages of 128 K,
+//            conflict-free ds_read_b128 fragment reads. Prefill.
+#include "capi_internal.h"
+#include "strix_common.h"
+
+namespace strix {
+namespace {
+
+enum Kind8 : int { kFp8Block = 0, kI8Token = 1, kI8Group = 2 };
+enum Epi : int { kEpiStore = 0, kEpiGated = 1, kEpiI32 = 2 };
+
+struct G8 {
+  const uint8_t* w;  // weight bytes [E][N][ldw]
+  int64_t ldw, w_es;
+  const float* sw;   // fp8: [E][ceil(N/128)][K/128]; i8: [E][N][G] (G may be 1)
+  int64_t sw_es, sw_ns, sw_ks;
+  const uint8_t* a;  // activation bytes [rows][lda]
+  int64_t lda;
+  const float* sa;   // [rows][K/128] (i8 token: [rows], sa_ks = 0)
+  int64_t sa_rs, sa_ks;
+  void* out;
+  int64_t ldo;
+  int out_f16;
+  int M, N, K;       // dense rows, weight rows per expert, K
+  int n_out;         // output columns (N, or N/2 when gated)
+  int gate_off;      // gated: first up row (= N/2)
+  const int32_t* sorted_ids;
+  int64_t sorted_len;
+  const int32_t* expert_ids;
+  const int32_t* num_post;
+  int num_slots, top_k;
+  const float* topk_w;
+  int w_excess128;   // weights stored as uint8b128 (byte - 128)
+};
+
+__device__ __forceinline__ u32x4 ldg128(const uint8_t* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+__device__ __forceinline__ u32x4 lds128(const uint8_t* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+__device__ __forceinline__ v8i cat8(const u32x4& lo, const u32x4& hi) {
+  v8i r;
+  r[0] = lo[0]; r[1] = lo[1]; r[2] = lo[2]; r[3] = lo[3];
+  r[4] = hi[0]; r[5] = hi[1]; r[6] = hi[2]; r[7] = hi[3];
+  return r;
+}
+__device__ __forceinline__ v4i lo4(const v8i& x) { v4i r; r[0] = x[0]; r[1] = x[1]; r[2] = x[2]; r[3] = x[3]; return r; }
+__device__ __forceinline__ v4i hi4(const v8i& x) { v4i r; r[0] = x[4]; r[1] = x[5]; r[2] = x[6]; r[3] = x[7]; return r; }
+__device__ __forceinline__ v8i flip80(const v8i& x) {
+  v8i r;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r[i] = x[i] ^ (int)0x80808080u;
+  return r;
+}
+
+// Token row of MFMA column m (block-relative index already added).
+template <bool MOE>
+__device__ __forceinline__ void token_row(const G8& p, int m, int& brow, int& orow, bool& valid) {
+  if constexpr (MOE) {
+    const int sid = (m < p.sorted_len) ? p.sorted_ids[m] : p.num_slots;
+    valid = sid >= 0 && sid < p.num_slots;
+    brow = valid ? sid / p.top_k : 0;
+    orow = sid;
+  } else {
+    valid = m < p.M;
+    brow = valid ? m : 0;
+    orow = m;
+  }
+}
+
+// Stores four consecutive output columns col0..col0+3 of row orow.
+__device__ __forceinline__ void store4(const G8& p, int orow, int col0, const float v[4]) {
+  if (p.out_f16) {
+    uint16_t* o = static_cast<uint16_t*>(p.out) + (int64_t)orow * p.ldo + col0;
+    if (col0 + 3 < p.n_out) {
+      *reinterpret_cast<uint2*>(o) = make_uint2(f32_to_f16_bits(v[0]) | (f32_to_f16_bits(v[1]) << 16),
+                                                f32_to_f16_bits(v[2]) | (f32_to_f16_bits(v[3]) << 16));
+    } else {
+      for (int i = 0; i < 4; ++i)
+        if (col0 + i < p.n_out) o[i] = (uint16_t)f32_to_f16_bits(v[i]);
+    }
+  } else {
+    uint16_t* o = static_cast<uint16_t*>(p.out) + (int64_t)orow * p.ldo + col0;
+    if (col0 + 3 < p.n_out) {
+      *reinterpret_cast<uint2*>(o) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+    } else {
+      for (int i = 0; i < 4; ++i)
+        if (col0 + i < p.n_out) o[i] = (uint16_t)f32_to_bf16_bits(v[i]);
+    }
+  }
+}
+__device__ __forceinline__ void store4_i32(const G8& p, int orow, int col0, const int v[4]) {
+  int* o = static_cast<int*>(p.out) + (int64_t)orow * p.ldo + col0;
+  if (col0 + 3 < p.n_out) {
+    *reinterpret_cast<int4*>(o) = make_int4(v[0], v[1], v[2], v[3]);
+  } else {
+    for (int i = 0; i < 4; ++i)
+      if (col0 + i < p.n_out) o[i] = v[i];
+  }
+}
+
+// Final epilogue for one output subtile: `g` holds the (gate) values, `u` the
+// up values when gated. I8 token values arrive as int32 bit patterns.
+template <int KIND, int EPI, int ACT, bool MOE>
+__device__ __forceinline__ void finish4(const G8& p, int orow, int brow, bool valid, int col0,
+                                        const float g[4], const float u[4]) {
+  if (!valid) return;
+  if constexpr (EPI == kEpiI32) {
+    int iv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) iv[i] = __float_as_int(g[i]);
+    store4_i32(p, orow, col0, iv);
+    return;
+  }
+  float v[4];
+  if constexpr (KIND == kI8Token) {
+    const float sa = p.sa[(int64_t)brow * p.sa_rs];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int n = min(col0 + i, p.N - 1);
+      v[i] = ((float)__float_as_int(g[i]) * sa) * p.sw[(int64_t)n * p.sw_ns];
+    }
+  } else if constexpr (EPI == kEpiGated) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = gate_act<ACT>(g[i]) * u[i];
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = g[i];
+  }
+  if constexpr (MOE) {
+    if (p.topk_w) {
+      const float tw = p.topk_w[orow];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] *= tw;
+    }
+  }
+  store4(p, orow, col0, v);
+}
+
+// ============================================================ stream8
+template <int KIND, int NT, int MT, int WAVES, bool MOE, int EPI, int ACT, int U>
+__global__ void __launch_bounds__(WAVES * 64) stream8_kernel(G8 p) {
+  constexpr int NTH = (EPI == kEpiGated) ? NT / 2 : NT;  // output subtiles
+  constexpr bool INT_ACC = (KIND == kI8Token);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r16 = lane & 15, g4 = lane >> 4;
+  const int m0 = blockIdx.y * (16 * MT);
+  int expert = 0;
+  if constexpr (MOE) {
+    if (m0 >= *p.num_post) return;
+    expert = p.expert_ids[blockIdx.y];
+    if (expert < 0) return;
+  }
+  const int nout0 = blockIdx.x * (16 * NTH);
+
+  int wrow0[NT];  // first weight row of each subtile
+#pragma unroll
+  for (int s = 0; s < NT; ++s) {
+    if constexpr (EPI == kEpiGated)
+      wrow0[s] = s < NTH ? nout0 + 16 * s : p.gate_off + nout0 + 16 * (s - NTH);
+    else
+      wrow0[s] = nout0 + 16 * s;
+  }
+  const uint8_t* wbase = p.w + (int64_t)expert * p.w_es;
+  const uint8_t* wp[NT];
+#pragma unroll
+  for (int s = 0; s < NT; ++s) {
+    const int r = min(wrow0[s] + r16, p.N - 1);
+    wp[s] = wbase + (int64_t)r * p.ldw + 16 * g4;
+  }
+  int brow[MT], orow[MT];
+  bool bval[MT];
+  const uint8_t* ap[MT];
+  const float* sap[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    token_row<MOE>(p, m0 + 16 * t + r16, brow[t], orow[t], bval[t]);
+    ap[t] = p.a + (int64_t)brow[t] * p.lda + 16 * g4;
+    sap[t] = p.sa + (int64_t)brow[t] * p.sa_rs;
+  }
+  const float* swb = p.sw + (int64_t)expert * p.sw_es;
+
+  const int nks = p.K >> 7;
+  const int per = (nks + WAVES - 1) / WAVES;
+  const int kb0 = min(nks, wave * per), kb1 = min(nks, kb0 + per);
+
+  v4f acc[NT][MT];
+  v4i acci[NT][MT];
+#pragma unroll
+  for (int s = 0; s < NT; ++s)
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      acc[s][t] = v4f{0.f, 0.f, 0.f, 0.f};
+      acci[s][t] = v4i{0, 0, 0, 0};
+    }
+
+  auto step = [&](int kb, const v8i (&af)[NT], const v8i (&bf)[MT]) {
+    if constexpr (KIND == kFp8Block) {
+      float sc_sw[NT];
+#pragma unroll
+      for (int s = 0; s < NT; ++s) sc_sw[s] = swb[(int64_t)(wrow0[s] >> 7) * p.sw_ns + (int64_t)kb * p.sw_ks];
+      float sc_sa[MT];
+#pragma unroll
+      for (int t = 0; t < MT; ++t) sc_sa[t] = sap[t][(int64_t)kb * p.sa_ks];
+#pragma unroll
+      for (int s = 0; s < NT; ++s)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          const v4f part = mfma_fp8(af[s], bf[t], v4f{0.f, 0.f, 0.f, 0.f});
+          const float c = sc_sw[s] * sc_sa[t];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[s][t][i] = fmaf(part[i], c, acc[s][t][i]);
+        }
+    } else if constexpr (KIND == kI8Token) {
+#pragma unroll
+      for (int s = 0; s < NT; ++s)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          acci[s][t] = mfma_i8(lo4(af[s]), lo4(bf[t]), acci[s][t]);
+          acci[s][t] = mfma_i8(hi4(af[s]), hi4(bf[t]), acci[s][t]);
+        }
+    } else {  // kI8Group
+      float sc_sa[MT];
+#pragma unroll
+      for (int t = 0; t < MT; ++t) sc_sa[t] = sap[t][(int64_t)kb * p.sa_ks];
+#pragma unroll
+      for (int s = 0; s < NT; ++s) {
+        float sw4[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int n = min(wrow0[s] + 4 * g4 + i, p.N - 1);
+          sw4[i] = swb[(int64_t)n * p.sw_ns + (int64_t)kb * p.sw_ks];
+        }
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          v4i part = mfma_i8(lo4(af[s]), lo4(bf[t]), v4i{0, 0, 0, 0});
+          part = mfma_i8(hi4(af[s]), hi4(bf[t]), part);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[s][t][i] = fmaf((float)part[i], sw4[i] * sc_sa[t], acc[s][t][i]);
+        }
+      }
+    }
+  };
+
+  auto load = [&](int kb, v8i (&af)[NT], v8i (&bf)[MT]) {
+    const int64_t ko = (int64_t)kb * 128;
+#pragma unroll
+    for (int s = 0; s < NT; ++s) {
+      af[s] = cat8(ldg128(wp[s] + ko), ldg128(wp[s] + ko + 64));
+      if (p.w_excess128) af[s] = flip80(af[s]);
+    }
+#pragma unroll
+    for (int t = 0; t < MT; ++t) bf[t] = cat8(ldg128(ap[t] + ko), ldg128(ap[t] + ko + 64));
+  };
+
+  int kb = kb0;
+  for (; kb + U <= kb1; kb += U) {
+    v8i af[U][NT], bf[U][MT];
+#pragma unroll
+    for (int u = 0; u < U; ++u) load(kb + u, af[u], bf[u]);
+#pragma unroll
+    for (int u = 0; u < U; ++u) step(kb + u, af[u], bf[u]);
+  }
+  for (; kb < kb1; ++kb) {
+    v8i af[NT], bf[MT];
+    load(kb, af, bf);
+    step(kb, af, bf);
+  }
+
+  // Cross-wave reduction: red[w][tile][i][lane].
+  constexpr int TILES = NT * MT;
+  __shared__ float red[WAVES > 1 ? WAVES * TILES * 4 * 64 : 1];
+  if constexpr (WAVES > 1) {
+#pragma unroll
+    for (int s = 0; s < NT; ++s)
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float v = INT_ACC ? __int_as_float(acci[s][t][i]) : acc[s][t][i];
+          red[((wave * TILES + s * MT + t) * 4 + i) * 64 + lane] = v;
+        }
+    __syncthreads();
+  }
+  // Output subtile o = (so, t) finished by wave o % WAVES.
+#pragma unroll
+  for (int so = 0; so < NTH; ++so)
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      const int o = so * MT + t;
+      if (WAVES > 1 && (o % WAVES) != wave) continue;
+      float g[4], u[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if constexpr (WAVES > 1) {
+          float sg = 0.f, su = 0.f;
+          int ig = 0, iu = 0;
+          for (int w = 0; w < WAVES; ++w) {
+            const float vg = red[((w * TILES + so * MT + t) * 4 + i) * 64 + lane];
+            if (INT_ACC) ig += __float_as_int(vg); else sg += vg;
+            if constexpr (EPI == kEpiGated) {
+              const float vu = red[((w * TILES + (so + NTH) * MT + t) * 4 + i) * 64 + lane];
+              if (INT_ACC) iu += __float_as_int(vu); else su += vu;
+            }
+          }
+          g[i] = INT_ACC ? __int_as_float(ig) : sg;
+          u[i] = INT_ACC ? __int_as_float(iu) : su;
+        } else {
+          g[i] = INT_ACC ? __int_as_float(acci[so][t][i]) : acc[so][t][i];
+          if constexpr (EPI == kEpiGated) u[i] = INT_ACC ? __int_as_float(acci[so + NTH][t][i]) : acc[so + NTH][t][i];
+          else u[i] = 0.f;
+        }
+      }
+      finish4<KIND, EPI, ACT, MOE>(p, orow[t], brow[t], bval[t], nout0 + 16 * so + 4 * g4, g, u);
+    }
+}
+
+// ============================================================ tiled8
+// Fragment-native LDS stage: region q = 2*subtile + half holds, at byte
+// 16*l, the 16 bytes that lane l feeds the MFMA for that (subtile, half).
+// Subtiles 0..SA-1 are weight rows, SA..SA+SB-1 token rows; after them the
+// stage keeps BM fp32 activation scales.
+template <int KIND, int BM, int BN, int WM, int WN, bool MOE, int EPI, int ACT>
+__global__ void __launch_bounds__(WM * WN * 64) tiled8_kernel(G8 p, int tiles_m, int tiles_n, int group_m) {
+  constexpr int W = WM * WN;
+  constexpr int TM = BM / WM, TN = BN / WN;
+  constexpr int MT = TM / 16, NT = TN / 16;
+  constexpr int SA = BN / 16, SB = BM / 16;
+  constexpr int NQ = 2 * (SA + SB);              // 1 KiB copies per stage
+  constexpr int QPW = (NQ + W - 1) / W;          // copies per wave
+  constexpr bool HAS_SA = (KIND != kI8Token);
+  constexpr int SA_BYTES = HAS_SA ? BM * 4 : 0;
+  constexpr int STAGE = NQ * 1024 + SA_BYTES;
+  constexpr bool GATED = (EPI == kEpiGated);
+  constexpr int NTH = GATED ? NT / 2 : NT;
+  constexpr bool INT_ACC = (KIND == kI8Token);
+  static_assert(BM % 64 == 0 || !HAS_SA, "scale staging uses 64-row copies");
+  static_assert(!GATED || (NT % 2 == 0), "gated wave tiles pair gate and up subtiles");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGE];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r16 = lane & 15, g4 = lane >> 4;
+  const int wm = wave % WM, wn = wave / WM;
+
+  int tm, tn, expert = 0;
+  if constexpr (MOE) {
+    tn = blockIdx.x;
+    tm = blockIdx.y;
+    if (tm * BM >= *p.num_post) return;
+    expert = p.expert_ids[tm];
+    if (expert < 0) return;
+  } else {
+    // XCD-aware order: the hardware deals block b to XCD b % 8; give each
+    // XCD a contiguous run of tiles, then walk them in group_m-tall columns.
+    const int nblk = tiles_m * tiles_n;
+    int b = blockIdx.x;
+    if ((nblk & 7) == 0) b = (b & 7) * (nblk >> 3) + (b >> 3);
+    const int per_group = group_m * tiles_n;
+    const int grp = b / per_group;
+    const int first_m = grp * group_m;
+    const int gm = min(tiles_m - first_m, group_m);
+    const int in = b - grp * per_group;
+    tm = first_m + in % gm;
+    tn = in / gm;
+  }
+  const int m0 = tm * BM;
+  // Weight row of LDS weight subtile j.
+  auto wrow_of = [&](int j) -> int {
+    if constexpr (GATED) {
+      const int base = tn * (BN / 2);
+      return j < SA / 2 ? base + 16 * j : p.gate_off + base + 16 * (j - SA / 2);
+    } else {
+      return tn * BN + 16 * j;
+    }
+  };
+
+  // Per-wave copy slots: fixed global row pointers, advanced 128 B per stage.
+  const uint8_t* wbase = p.w + (int64_t)expert * p.w_es;
+  const uint8_t* qptr[QPW];
+#pragma unroll
+  for (int j = 0; j < QPW; ++j) {
+    const int q = wave + W * j;
+    const int sub = q >> 1, half = q & 1;
+    const uint8_t* ptr = nullptr;
+    if (q < NQ) {
+      if (sub < SA) {
+        const int r = min(wrow_of(sub) + r16, p.N - 1);
+        ptr = wbase + (int64_t)r * p.ldw;
+      } else {
+        int br, orw;
+        bool v;
+        token_row<MOE>(p, m0 + 16 * (sub - SA) + r16, br, orw, v);
+        ptr = p.a + (int64_t)br * p.lda;
+      }
+      ptr += 64 * half + 16 * g4;
+    }
+    qptr[j] = ptr;
+  }
+  const float* saptr = nullptr;  // scale copy slot: wave w < BM/64 copies rows 64w..64w+63
+  if constexpr (HAS_SA) {
+    if (wave < BM / 64) {
+      int br, orw;
+      bool v;
+      token_row<MOE>(p, m0 + 64 * wave + lane, br, orw, v);
+      saptr = p.sa + (int64_t)br * p.sa_rs;
+    }
+  }
+
+  auto issue = [&](int kb, int buf) {
+    uint8_t* st = smem + buf * STAGE;
+#pragma unroll
+    for (int j = 0; j < QPW; ++j) {
+      const int q = wave + W * j;
+      if (q < NQ) g2l_b128(qptr[j] + (int64_t)kb * 128, st + q * 1024);
+    }
+    if constexpr (HAS_SA) {
+      if (wave < BM / 64) g2l_b32(saptr + (int64_t)kb * p.sa_ks, st + NQ * 1024 + wave * 256);
+    }
+  };
+
+  // Wave's A subtiles (LDS indices) and their first weight rows.
+  int aidx[NT], arow0[NT];
+#pragma unroll
+  for (int s = 0; s < NT; ++s) {
+    if constexpr (GATED)
+      aidx[s] = s < NTH ? wn * NTH + s : SA / 2 + wn * NTH + (s - NTH);
+    else
+      aidx[s] = wn * NT + s;
+    arow0[s] = wrow_of(aidx[s]);
+  }
+  const float* swb = p.sw + (int64_t)expert * p.sw_es;
+
+  v4f acc[NT][MT];
+  v4i acci[NT][MT];
+#pragma unroll
+  for (int s = 0; s < NT; ++s)
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      acc[s][t] = v4f{0.f, 0.f, 0.f, 0.f};
+      acci[s][t] = v4i{0, 0, 0, 0};
+    }
+
+  const int nkb = p.K >> 7;
+  issue(0, 0);
+  for (int kb = 0; kb < nkb; ++kb) {
+    const int buf = kb & 1;
+    wait_vmem();
+    __syncthreads();
+    if (kb + 1 < nkb) issue(kb + 1, buf ^ 1);
+    const uint8_t* st = smem + buf * STAGE;
+    v8i bf[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      const int q = 2 * (SA + wm * MT + t);
+      bf[t] = cat8(lds128(st + q * 1024 + 16 * lane), lds128(st + (q + 1) * 1024 + 16 * lane));
+    }
+    float sa_t[MT];
+    if constexpr (HAS_SA) {
+      const float* sl = reinterpret_cast<const float*>(st + NQ * 1024);
+#pragma unroll
+      for (int t = 0; t < MT; ++t) sa_t[t] = sl[wm * TM + 16 * t + r16];
+    }
+#pragma unroll
+    for (int s = 0; s < NT; ++s) {
+      const int q = 2 * aidx[s];
+      v8i af = cat8(lds128(st + q * 1024 + 16 * lane), lds128(st + (q + 1) * 1024 + 16 * lane));
+      if (p.w_excess128) af = flip80(af);
+      if constexpr (KIND == kFp8Block) {
+        const float sw = swb[(int64_t)(arow0[s] >> 7) * p.sw_ns + (int64_t)kb * p.sw_ks];
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          const v4f part = mfma_fp8(af, bf[t], v4f{0.f, 0.f, 0.f, 0.f});
+          const float c = sw * sa_t[t];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[s][t][i] = fmaf(part[i], c, acc[s][t][i]);
+        }
+      } else if constexpr (KIND == kI8Token) {
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          acci[s][t] = mfma_i8(lo4(af), lo4(bf[t]), acci[s][t]);
+          acci[s][t] = mfma_i8(hi4(af), hi4(bf[t]), acci[s][t]);
+        }
+      } else {
+        float sw4[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int n = min(arow0[s] + 4 * g4 + i, p.N - 1);
+          sw4[i] = swb[(int64_t)n * p.sw_ns + (int64_t)kb * p.sw_ks];
+        }
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          v4i part = mfma_i8(lo4(af), lo4(bf[t]), v4i{0, 0, 0, 0});
+          part = mfma_i8(hi4(af), hi4(bf[t]), part);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[s][t][i] = fmaf((float)part[i], sw4[i] * sa_t[t], acc[s][t][i]);
+        }
+      }
+    }
+  }
+
+  // Epilogue straight from registers.
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    int br, orw;
+    bool v;
+    token_row<MOE>(p, m0 + wm * TM + 16 * t + r16, br, orw, v);
+#pragma unroll
+    for (int so = 0; so < NTH; ++so) {
+      float g[4], u[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        g[i] = INT_ACC ? __int_as_float(acci[so][t][i]) : acc[so][t][i];
+        if constexpr (GATED) u[i] = acc[so + NTH][t][i];
+        else u[i] = 0.f;
+      }
+      const int col0 = GATED ? (tn * (BN / 2) + 16 * (wn * NTH + so) + 4 * g4)
+                             : (tn * BN + 16 * (wn * NT + so) + 4 * g4);
+      finish4<KIND, EPI, ACT, MOE>(p, orw, br, v, col0, g, u);
+    }
+  }
+}
+
+// ============================================================ launchers
+template <int KIND, int NT, int MT, int WAVES, bool MOE, int EPI, int ACT, int U>
+int launch_stream(const G8& p, int grid_y, hipStream_t st, const char* op) {
+  constexpr int NTH = (EPI == kEpiGated) ? NT / 2 : NT;
+  const int grid_x = (p.n_out + 16 * NTH - 1) / (16 * NTH);
+  hipLaunchKernelGGL((stream8_kernel<KIND, NT, MT, WAVES, MOE, EPI, ACT, U>), dim3(grid_x, grid_y),
+                     dim3(WAVES * 64), 0, st, p);
+  return check_launch(op);
+}
+
+template <int KIND, int BM, int BN, int WM, int WN, bool MOE, int EPI, int ACT>
+int launch_tiled(const G8& p, int grid_y_moe, hipStream_t st, const char* op) {
+  constexpr int COLS = (EPI == kEpiGated) ? BN / 2 : BN;
+  const int tiles_n = (p.n_out + COLS - 1) / COLS;
+  if constexpr (MOE) {
+    hipLaunchKernelGGL((tiled8_kernel<KIND, BM, BN, WM, WN, MOE, EPI, ACT>), dim3(tiles_n, grid_y_moe),
+                       dim3(WM * WN * 64), 0, st, p, 0, tiles_n, 0);
+  } else {
+    const int tiles_m = (p.M + BM - 1) / BM;
+    hipLaunchKernelGGL((tiled8_kernel<KIND, BM, BN, WM, WN, MOE, EPI, ACT>), dim3(tiles_m * tiles_n),
+                       dim3(WM * WN * 64), 0, st, p, tiles_m, tiles_n, 8);
+  }
+  return check_launch(op);
+}
+
+// Dense dispatch by M. cfg >= 0 pins one tile config (tile sweeps).
+template <int KIND, int EPI>
+int dense_dispatch(const G8& p, hipStream_t st, const char* op, int cfg) {
+  const int M = p.M;
+  if (cfg < 0) {
+    if (M <= 16) cfg = 0;
+    else if (M <= 32) cfg = 1;
+    else if (M <= 64) cfg = 2;
+    else if (M <= 256) cfg = 4;
+    else cfg = 5;
+  }
+  switch (cfg) {
+    case 0: return launch_stream<KIND, 1, 1, 8, false, EPI, kActSilu, 4>(p, (M + 15) / 16, st, op);
+    case 1: return launch_stream<KIND, 1, 2, 8, false, EPI, kActSilu, 4>(p, (M + 31) / 32, st, op);
+    case 2: return launch_stream<KIND, 1, 4, 4, false, EPI, kActSilu, 2>(p, (M + 63) / 64, st, op);
+    case 3: return launch_tiled<KIND, 128, 128, 2, 2, false, EPI, kActSilu>(p, 0, st, op);
+    case 4: return launch_tiled<KIND, 256, 64, 4, 2, false, EPI, kActSilu>(p, 0, st, op);
+    case 5: return launch_tiled<KIND, 256, 256, 4, 2, false, EPI, kActSilu>(p, 0, st, op);
+    case 6: return launch_tiled<KIND, 128, 256, 2, 2, false, EPI, kActSilu>(p, 0, st, op);
+    default: return set_error(STRIX_ERR_INVALID, "%s: cfg must be in 0..6, got %d", op, cfg);
+  }
+}
+
+// MoE dispatch by block_m (the sorted-id granularity).
+template <int KIND, int EPI, int ACT>
+int moe_dispatch(const G8& p, int block_m, int num_blocks, hipStream_t st, const char* op) {
+  switch (block_m) {
+    case 16: return launch_stream<KIND, (EPI == kEpiGated ? 2 : 1), 1, 4, true, EPI, ACT, 2>(p, num_blocks, st, op);
+    case 32: return launch_stream<KIND, (EPI == kEpiGated ? 2 : 1), 2, 4, true, EPI, ACT, 2>(p, num_blocks, st, op);
+    case 64: return launch_tiled<KIND, 64, 128, 1, 4, true, EPI, ACT>(p, num_blocks, st, op);
+    case 128: return launch_tiled<KIND, 128, 128, 2, 2, true, EPI, ACT>(p, num_blocks, st, op);
+    case 256: return launch_tiled<KIND, 256, 128, 4, 2, true, EPI, ACT>(p, num_blocks, st, op);
+    default: return set_error(STRIX_ERR_INVALID, "%s: block_m must be 16, 32, 64, 128 or 256, got %d", op, block_m);
+  }
+}
+
+int check_common(const char* op, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw,
+                 const void* a, const void* w) {
+  STRIX_REQUIRE(M >= 0 && N >= 0 && K >= 0, "%s: negative size", op);
+  STRIX_REQUIRE(K % 128 == 0, "%s: K must be a multiple of 128, got K=%lld", op, (long long)K);
+  STRIX_REQUIRE(ldw >= K && ldw % 16 == 0, "%s: weight row stride (%lld bytes) must be >= K and a multiple of 16",
+                op, (long long)ldw);
+  STRIX_REQUIRE(lda >= K && lda % 16 == 0, "%s: activation row stride must be >= K and a multiple of 16", op);
+  STRIX_REQUIRE(aligned(a, 16) && aligned(w, 16), "%s: operands must be 16-byte aligned", op);
+  STRIX_REQUIRE(M <= INT32_MAX && N <= INT32_MAX && K <= INT32_MAX, "%s: sizes overflow 32-bit indexing", op);
+  return STRIX_OK;
+}
+
+}  // namespace
+}  // namespace strix
+
+using namespace strix;
+
+extern "C" {
+
+int strix_fp8_w8a8_block_gemm(const uint8_t* qa, int64_t lda, const float* sa, int64_t sa_ld,
+                              const uint8_t* w, int64_t ldw, const float* sw, int64_t sw_ld,
+                              void* out, int64_t ldo, int out_dtype, int64_t M, int64_t N,
+                              int64_t K, int cfg, void* stream) {
+  const char* op = "fp8_w8a8_block_gemm";
+  int rc = check_common(op, M, N, K, lda, ldw, qa, w);
+  if (rc) return rc;
+  STRIX_REQUIRE(out_dtype == STRIX_BF16 || out_dtype == STRIX_F16, "%s: output must be bfloat16 or float16", op);
+  STRIX_REQUIRE(sa_ld >= K / 128 && sw_ld >= K / 128, "%s: scale row strides must be >= K/128", op);
+  STRIX_REQUIRE(ldo >= N && ldo % 4 == 0 && aligned(out, 8), "%s: output rows must be >= N, 8-byte aligned", op);
+  if (M == 0 || N == 0) return STRIX_OK;
+  STRIX_ARCH_GATE();
+  G8 p = {};
+  p.w = w; p.ldw = ldw; p.w_es = 0;
+  p.sw = sw; p.sw_es = 0; p.sw_ns = sw_ld; p.sw_ks = 1;
+  p.a = qa; p.lda = lda; p.sa = sa; p.sa_rs = sa_ld; p.sa_ks = 1;
+  p.out = out; p.ldo = ldo; p.out_f16 = out_dtype == STRIX_F16;
+  p.M = (int)M; p.N = (int)N; p.K = (int)K; p.n_out = (int)N;
+  return dense_dispatch<kFp8Block, kEpiStore>(p, as_stream(stream), op, cfg);
+}
+
+int strix_w8a8_int8_gemm(const int8_t* qa, int64_t lda, const float* sa, const int8_t* w, int64_t ldw,
+                         const float* sw, void* out, int64_t ldo, int out_dtype, int64_t M, int64_t N,
+                         int64_t K, int cfg, void* stream) {
+  const char* op = "w8a8_scaled_mm";
+  int rc = check_common(op, M, N, K, lda, ldw, qa, w);
+  if (rc) return rc;
+  STRIX_REQUIRE(out_dtype == STRIX_BF16 || out_dtype == STRIX_F16 || out_dtype == STRIX_I32,
+                "%s: output must be bfloat16, float16 or int32", op);
+  STRIX_REQUIRE(ldo >= N && ldo % 4 == 0 && aligned(out, 16), "%s: output rows must be >= N, 16-byte aligned", op);
+  if (M == 0 || N == 0) return STRIX_OK;
+  STRIX_ARCH_GATE();
+  G8 p = {};
+  p.w = reinterpret_cast<const uint8_t*>(w); p.ldw = ldw;
+  p.sw = sw; p.sw_ns = 1;
+  p.a = reinterpret_cast<const uint8_t*>(qa); p.lda = lda; p.sa = sa; p.sa_rs = 1; p.sa_ks = 0;
+  p.out = out; p.ldo = ldo; p.out_f16 = out_dtype == STRIX_F16;
+  p.M = (int)M; p.N = (int)N; p.K = (int)K; p.n_out = (int)N;
+  if (out_dtype == STRIX_I32) return dense_dispatch<kI8Token, kEpiI32>(p, as_stream(stream), op, cfg);
+  STRIX_REQUIRE(sa != nullptr && sw != nullptr, "%s: scales are required for a float output", op);
+  return dense_dispatch<kI8Token, kEpiStore>(p, as_stream(stream), op, cfg);
+}
+
+int strix_w8a8_int8_group_gemm(const int8_t* qa, int64_t lda, const float* sa, int64_t sa_ld,
+                               const uint8_t* w, int64_t ldw, int w_excess128, const float* sw,
+                               int64_t sw_ns, int64_t sw_gs, void* out, int64_t ldo, int out_dtype,
+                               int64_t M, int64_t N, int64_t K, int cfg, void* stream) {
+  const char* op = "w8a8_wmma_gemm";
+  int rc = check_common(op, M, N, K, lda, ldw, qa, w);
+  if (rc) return rc;
+  STRIX_REQUIRE(out_dtype == STRIX_BF16 || out_dtype == STRIX_F16, "%s: output must be bfloat16 or float16", op);
+  STRIX_REQUIRE(ldo >= N && ldo % 4 == 0 && aligned(out, 8), "%s: output rows must be >= N, 8-byte aligned", op);
+  if (M == 0 || N == 0) return STRIX_OK;
+  STRIX_ARCH_GATE();
+  G8 p = {};
+  p.w = w; p.ldw = ldw; p.w_excess128 = w_excess128;
+  p.sw = sw; p.sw_ns = sw_ns; p.sw_ks = sw_gs;
+  p.a = reinterpret_cast<const uint8_t*>(qa); p.lda = lda; p.sa = sa; p.sa_rs = sa_ld; p.sa_ks = 1;
+  p.out = out; p.ldo = ldo; p.out_f16 = out_dtype == STRIX_F16;
+  p.M = (int)M; p.N = (int)N; p.K = (int)K; p.n_out = (int)N;
+  return dense_dispatch<kI8Group, kEpiStore>(p, as_stream(stream), op, cfg);
+}
+
+int strix_moe_gemm_fp8_w8a8(void* c, int64_t ldc, int c_dtype, const uint8_t* qa, int64_t lda,
+                            const float* sa, int64_t sa_ld, const uint8_t* w, int64_t w_es, int64_t ldw,
+                            const float* sw, int64_t sw_es, int64_t sw_ns, const int32_t* sorted_ids,
+                            int64_t sorted_len, const int32_t* expert_ids, int64_t num_blocks,
+                            const int32_t* num_post, const float* topk_weights, int64_t num_slots,
+                            int64_t top_k, int64_t block_m, int silu_mul, int activation, int64_t N,
+                            int64_t K, void* stream) {
+  const char* op = "moe_gemm_fp8_w8a8";
+  int rc = check_common(op, num_slots, N, K, lda, ldw, qa, w);
+  if (rc) return rc;
+  STRIX_REQUIRE(c_dtype == STRIX_BF16 || c_dtype == STRIX_F16, "%s: output must be bfloat16 or float16", op);
+  STRIX_REQUIRE(top_k >= 1, "%s: top_k must be >= 1", op);
+  STRIX_REQUIRE(num_blocks * block_m >= sorted_len, "%s: expert_ids.numel() * block_m must cover sorted_ids", op);
+  STRIX_REQUIRE(!silu_mul || N % 32 == 0, "%s: gated N must be a multiple of 32", op);
+  STRIX_REQUIRE(N % 16 == 0, "%s: N must be a multiple of 16", op);
+  STRIX_REQUIRE(activation == kActSilu || activation == kActGeluTanh, "%s: unknown activation", op);
+  const int64_t n_out = silu_mul ? N / 2 : N;
+  STRIX_REQUIRE(ldc >= n_out && ldc % 4 == 0 && aligned(c, 8), "%s: output rows must be >= %lld, 8-byte aligned",
+                op, (long long)n_out);
+  STRIX_REQUIRE(!silu_mul || (N / 2) % 128 == 0, "%s: gated FP8-block N/2 must be a multiple of 128", op);
+  if (num_blocks == 0 || num_slots == 0 || N == 0) return STRIX_OK;
+  STRIX_ARCH_GATE();
+  G8 p = {};
+  p.w = w; p.ldw = ldw; p.w_es = w_es;
+  p.sw = sw; p.sw_es = sw_es; p.sw_ns = sw_ns; p.sw_ks = 1;
+  p.a = qa; p.lda = lda; p.sa = sa; p.sa_rs = sa_ld; p.sa_ks = 1;
+  p.out = c; p.ldo = ldc; p.out_f16 = c_dtype == STRIX_F16;
+  p.M = (int)num_slots; p.N = (int)N; p.K = (int)K; p.n_out = (int)n_out; p.gate_off = (int)(N / 2);
+  p.sorted_ids = sorted_ids; p.sorted_len = sorted_len; p.expert_ids = expert_ids; p.num_post = num_post;
+  p.num_slots = (int)num_slots; p.top_k = (int)top_k; p.topk_w = topk_weights;
+  hipStream_t st = as_stream(stream);
+  const int nb = (int)num_blocks, bm = (int)block_m;
+  if (silu_mul) {
+    if (activation == kActGeluTanh) return moe_dispatch<kFp8Block, kEpiGated, kActGeluTanh>(p, bm, nb, st, op);
+    return moe_dispatch<kFp8Block, kEpiGated, kActSilu>(p, bm, nb, st, op);
+  }
+  return moe_dispatch<kFp8Block, kEpiStore, kActSilu>(p, bm, nb, st, op);
+}
+
+}  // extern "C"

@@ -1,0 +1,204 @@
+// SPDX-License-Identifier: MIT
+// Activation quantizers in front of the 8-bit MFMA GEMMs.
+//
+//   int8 per token      s[m]    = max_k |x[m,k]| / 127   (1 if the row is 0)
+//                       q[m,k]  = clamp(rint(x[m,k] / s[m]), -127, 127)
+//   int8 per 128-group  s[m,g]  = max_{k in g} |x[m,k]| / 127 (1 if 0), same q
+//                       (reference convention: csrc/gemm/w8a8_wmma_gemm.hip:15-21,
+//                        tests/test_moe_w4a8.py:24-36)
+//   e4m3 per 128-group  s[m,g]  = max_{k in g} |x[m,k]| / 448 (1 if 0)
+//                       q[m,k]  = e4m3_rne(x[m,k] / s[m,g])
+//
+// The division is IEEE (correctly rounded), so the CPU oracle reproduces q
+// bit for bit. Each lane owns 8 consecutive elements (one 16-byte load); a
+// 128-group is 16 lanes, so the group max is a 16-lane butterfly.
+#include "capi_internal.h"
+#include "strix_common.h"
+
+namespace strix {
+namespace {
+
+template <bool F16>
+__device__ __forceinline__ void load8(const uint16_t* p, float v[8]) {
+  const u32x4 raw = *reinterpret_cast<const u32x4*>(p);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = act_to_f32<F16>(raw[i] & 0xffffu);
+    v[2 * i + 1] = act_to_f32<F16>(raw[i] >> 16);
+  }
+}
+
+__device__ __forceinline__ int q_i8(float x, float s) {
+  float r = __builtin_rintf(__fdiv_rn(x, s));
+  r = fminf(fmaxf(r, -127.0f), 127.0f);
+  return (int)r;
+}
+
+// One 256-thread block per row.
+template <bool F16>
+__global__ void __launch_bounds__(256)
+    int8_quant_token_kernel(const uint16_t* __restrict__ x, int64_t ldx, int8_t* __restrict__ q,
+                            int64_t ldq, float* __restrict__ s, int K) {
+  __shared__ float red[4];
+  const int64_t m = blockIdx.x;
+  const uint16_t* xr = x + m * ldx;
+  float mx = 0.0f;
+  for (int k = threadIdx.x * 8; k < K; k += 256 * 8) {
+    float v[8];
+    load8<F16>(xr + k, v);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(v[i]));
+  }
+  mx = wave_max(mx);
+  if (lane_id() == 0) red[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float sc = mx > 0.0f ? __fdiv_rn(mx, 127.0f) : 1.0f;
+  if (threadIdx.x == 0) s[m] = sc;
+  int8_t* qr = q + m * ldq;
+  for (int k = threadIdx.x * 8; k < K; k += 256 * 8) {
+    float v[8];
+    load8<F16>(xr + k, v);
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) lo |= (uint32_t)(q_i8(v[i], sc) & 0xff) << (8 * i);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) hi |= (uint32_t)(q_i8(v[4 + i], sc) & 0xff) << (8 * i);
+    *reinterpret_cast<uint2*>(qr + k) = make_uint2(lo, hi);
+  }
+}
+
+// 128-element groups. Thread t of the grid handles elements [8t, 8t+8) of
+// the flattened [M, K] view (row-major by groups), 16 lanes per group.
+// FP8 selects the e4m3 quantizer, otherwise int8.
+template <bool F16, bool FP8>
+__global__ void __launch_bounds__(256)
+    quant_group128_kernel(const uint16_t* __restrict__ x, int64_t ldx, uint8_t* __restrict__ q,
+                          int64_t ldq, float* __restrict__ s, int64_t lds, int groups_per_row,
+                          int64_t total_groups) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t grp = t >> 4;
+  const int sub = t & 15;
+  const bool live = grp < total_groups;
+  const int64_t m = live ? grp / groups_per_row : 0;
+  const int g = live ? (int)(grp % groups_per_row) : 0;
+  const int64_t k = (int64_t)g * 128 + sub * 8;
+  float v[8];
+  if (live) {
+    load8<F16>(x + m * ldx + k, v);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+  }
+  float mx = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(v[i]));
+#pragma unroll
+  for (int o = 8; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
+  const float qmax = FP8 ? 448.0f : 127.0f;
+  const float sc = mx > 0.0f ? __fdiv_rn(mx, qmax) : 1.0f;
+  if (!live) return;
+  if (sub == 0) s[m * lds + g] = sc;
+  uint32_t lo = 0, hi = 0;
+  if constexpr (FP8) {
+    int w0 = 0, w1 = 0;
+    w0 = cvt_pk_e4m3<false>(__fdiv_rn(v[0], sc), __fdiv_rn(v[1], sc), w0);
+    w0 = cvt_pk_e4m3<true>(__fdiv_rn(v[2], sc), __fdiv_rn(v[3], sc), w0);
+    w1 = cvt_pk_e4m3<false>(__fdiv_rn(v[4], sc), __fdiv_rn(v[5], sc), w1);
+    w1 = cvt_pk_e4m3<true>(__fdiv_rn(v[6], sc), __fdiv_rn(v[7], sc), w1);
+    lo = (uint32_t)w0;
+    hi = (uint32_t)w1;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) lo |= (uint32_t)(q_i8(v[i], sc) & 0xff) << (8 * i);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) hi |= (uint32_t)(q_i8(v[4 + i], sc) & 0xff) << (8 * i);
+  }
+  *reinterpret_cast<uint2*>(q + m * ldq + k) = make_uint2(lo, hi);
+}
+
+int check_act(const char* op, const void* x, int x_dtype, int64_t ldx, const void* q, int64_t ldq,
+              int64_t M, int64_t K) {
+  STRIX_REQUIRE(x_dtype == STRIX_BF16 || x_dtype == STRIX_F16,
+                "%s: activation must be float16 or bfloat16", op);
+  STRIX_REQUIRE(M >= 0 && K >= 0, "%s: negative size", op);
+  STRIX_REQUIRE(K % 8 == 0, "%s: K must be a multiple of 8, got K=%lld", op, (long long)K);
+  STRIX_REQUIRE(ldx >= K && ldx % 8 == 0, "%s: activation row stride must be >= K and a multiple of 8",
+                op);
+  STRIX_REQUIRE(ldq >= K && ldq % 8 == 0, "%s: output row stride must be >= K and a multiple of 8", op);
+  STRIX_REQUIRE(M == 0 || (aligned(x, 16) && aligned(q, 8)),
+                "%s: activation must be 16-byte aligned and output 8-byte aligned", op);
+  STRIX_REQUIRE(M <= INT32_MAX && K <= INT32_MAX, "%s: sizes overflow 32-bit indexing", op);
+  return STRIX_OK;
+}
+
+}  // namespace
+}  // namespace strix
+
+using namespace strix;
+
+extern "C" {
+
+int strix_int8_quant_per_token(const void* x, int x_dtype, int64_t ldx, int8_t* q, int64_t ldq,
+                               float* s, int64_t M, int64_t K, void* stream) {
+  int rc = check_act("int8_quant_per_token", x, x_dtype, ldx, q, ldq, M, K);
+  if (rc) return rc;
+  if (M == 0) return STRIX_OK;
+  STRIX_REQUIRE(K > 0, "int8_quant_per_token: K must be positive");
+  STRIX_ARCH_GATE();
+  const uint16_t* xp = static_cast<const uint16_t*>(x);
+  if (x_dtype == STRIX_F16)
+    hipLaunchKernelGGL(int8_quant_token_kernel<true>, dim3((unsigned)M), dim3(256), 0,
+                       as_stream(stream), xp, ldx, q, ldq, s, (int)K);
+  else
+    hipLaunchKernelGGL(int8_quant_token_kernel<false>, dim3((unsigned)M), dim3(256), 0,
+                       as_stream(stream), xp, ldx, q, ldq, s, (int)K);
+  return check_launch("int8_quant_per_token");
+}
+
+static int quant_group128(const char* op, bool fp8, const void* x, int x_dtype, int64_t ldx,
+                          void* q, int64_t ldq, float* s, int64_t lds, int64_t M, int64_t K,
+                          void* stream) {
+  int rc = check_act(op, x, x_dtype, ldx, q, ldq, M, K);
+  if (rc) return rc;
+  STRIX_REQUIRE(K % 128 == 0, "%s: K must be a multiple of 128, got K=%lld", op, (long long)K);
+  STRIX_REQUIRE(lds >= K / 128, "%s: scale row stride must be >= K/128", op);
+  if (M == 0 || K == 0) return STRIX_OK;
+  STRIX_ARCH_GATE();
+  const int64_t groups = M * (K / 128);
+  const int64_t threads = groups * 16;
+  const unsigned blocks = (unsigned)((threads + 255) / 256);
+  const uint16_t* xp = static_cast<const uint16_t*>(x);
+  uint8_t* qp = static_cast<uint8_t*>(q);
+  const int gpr = (int)(K / 128);
+  hipStream_t st = as_stream(stream);
+  if (fp8) {
+    if (x_dtype == STRIX_F16)
+      hipLaunchKernelGGL((quant_group128_kernel<true, true>), dim3(blocks), dim3(256), 0, st, xp,
+                         ldx, qp, ldq, s, lds, gpr, groups);
+    else
+      hipLaunchKernelGGL((quant_group128_kernel<false, true>), dim3(blocks), dim3(256), 0, st, xp,
+                         ldx, qp, ldq, s, lds, gpr, groups);
+  } else {
+    if (x_dtype == STRIX_F16)
+      hipLaunchKernelGGL((quant_group128_kernel<true, false>), dim3(blocks), dim3(256), 0, st, xp,
+                         ldx, qp, ldq, s, lds, gpr, groups);
+    else
+      hipLaunchKernelGGL((quant_group128_kernel<false, false>), dim3(blocks), dim3(256), 0, st, xp,
+                         ldx, qp, ldq, s, lds, gpr, groups);
+  }
+  return check_launch(op);
+}
+
+int strix_int8_quant_group128(const void* x, int x_dtype, int64_t ldx, int8_t* q, int64_t ldq,
+                              float* s, int64_t lds, int64_t M, int64_t K, void* stream) {
+  return quant_group128("int8_quant_group128", false, x, x_dtype, ldx, q, ldq, s, lds, M, K,
+                        stream);
+}
+
+int strix_fp8_quant_group128(const void* x, int x_dtype, int64_t ldx, uint8_t* q, int64_t ldq,
+                             float* s, int64_t lds, int64_t M, int64_t K, void* stream) {
+  return quant_group128("fp8_quant_group128", true, x, x_dtype, ldx, q, ldq, s, lds, M, K, stream);
+}
+
+}  // extern "C"

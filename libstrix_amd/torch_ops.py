@@ -1,0 +1,422 @@
+# SPDX-License-Identifier: MIT
+"""torch.ops.strix.* on top of the C ABI.
+
+The reference registers its ops from C++ (csrc/torch_ops.cpp:179-344). Here
+the schemas are defined from Python with torch.library and each CUDA-key
+implementation is a thin call into libstrix_amd/_strix_amd.so through ctypes,
+on the current stream, with no host synchronization (so the ops are HIP-graph
+capturable). Reference schemas are kept byte-identical; the ops this build
+adds for the W8A8 and zero-point numerics are additive.
+
+Every op raises RuntimeError on a bad argument (message from the library) and
+when the library is not built; there is no CPU or PyTorch fallback.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from libstrix_amd import _lib
+
+_LIB = torch.library.Library("strix", "DEF")
+SCHEMAS: dict[str, str] = {}
+_ACT = {"silu": _lib.ACT_SILU, "gelu_tanh": _lib.ACT_GELU_TANH}
+
+
+def _define(schema: str):
+    name = schema.split("(", 1)[0]
+    SCHEMAS[name] = schema
+    _LIB.define(schema)
+
+    def deco(fn):
+        _LIB.impl(name, fn, "CUDA")
+        return fn
+
+    return deco
+
+
+def _fake(name: str):
+    return torch.library.register_fake(f"strix::{name}")
+
+
+# ----------------------------------------------------------------- helpers
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _act_code(t: torch.Tensor) -> int:
+    if t.dtype == torch.bfloat16:
+        return _lib.BF16
+    if t.dtype == torch.float16:
+        return _lib.F16
+    raise RuntimeError(f"Activation must be float16 or bfloat16, got {t.dtype}")
+
+
+def _out_code(dtype: torch.dtype) -> int:
+    return {torch.bfloat16: _lib.BF16, torch.float16: _lib.F16, torch.int32: _lib.I32}[dtype]
+
+
+def _check(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _rowmajor(t: torch.Tensor, what: str) -> None:
+    _check(t.dim() == 2 and t.stride(1) == 1, f"{what} must be 2-D and contiguous in dim 1")
+
+
+def _activation(name: str) -> int:
+    _check(name in _ACT, f"activation must be 'silu' or 'gelu_tanh', got {name!r}")
+    return _ACT[name]
+
+
+# ----------------------------------------------------------------- quant
+@_define("int8_quant_per_token(Tensor x) -> (Tensor, Tensor)")
+def int8_quant_per_token(x):
+    _rowmajor(x, "x")
+    m, k = x.shape
+    q = torch.empty((m, k), dtype=torch.int8, device=x.device)
+    s = torch.empty((m,), dtype=torch.float32, device=x.device)
+    _lib.call("strix_int8_quant_per_token", _ptr(x), _act_code(x), x.stride(0), _ptr(q), k, _ptr(s), m, k,
+              _stream(x))
+    return q, s
+
+
+@_fake("int8_quant_per_token")
+def _(x):
+    return x.new_empty(x.shape, dtype=torch.int8), x.new_empty((x.size(0),), dtype=torch.float32)
+
+
+@_define("fp8_quant_group128(Tensor x) -> (Tensor, Tensor)")
+def fp8_quant_group128(x):
+    _rowmajor(x, "x")
+    m, k = x.shape
+    q = torch.empty((m, k), dtype=torch.float8_e4m3fn, device=x.device)
+    s = torch.empty((m, k // 128), dtype=torch.float32, device=x.device)
+    _lib.call("strix_fp8_quant_group128", _ptr(x), _act_code(x), x.stride(0), _ptr(q), k, _ptr(s), max(k // 128, 1),
+              m, k, _stream(x))
+    return q, s
+
+
+@_fake("fp8_quant_group128")
+def _(x):
+    return (x.new_empty(x.shape, dtype=torch.float8_e4m3fn),
+            x.new_empty((x.size(0), x.size(1) // 128), dtype=torch.float32))
+
+
+# Reference schema: csrc/torch_ops.cpp:217 (int8 per (row, 128-group)).
+@_define("moe_act_quant_i8(Tensor x, Tensor(a!) q, Tensor(b!) sa) -> ()")
+def moe_act_quant_i8(x, q, sa):
+    _rowmajor(x, "x")
+    m, k = x.shape
+    _check(q.dtype == torch.int8 and tuple(q.shape) == (m, k) and q.stride(1) == 1, "q must be int8 [M, K]")
+    _check(sa.dtype == torch.float32 and tuple(sa.shape) == (m, k // 128) and sa.stride(1) == 1,
+           "sa must be float32 [M, K/128]")
+    _lib.call("strix_int8_quant_group128", _ptr(x), _act_code(x), x.stride(0), _ptr(q), q.stride(0), _ptr(sa),
+              sa.stride(0), m, k, _stream(x))
+
+
+@_fake("moe_act_quant_i8")
+def _(x, q, sa):
+    return None
+
+
+# ----------------------------------------------------------------- int8 W8A8
+def _i8_gemm(qa, sa, w, sw, out_dtype, cfg):
+    _rowmajor(qa, "qa")
+    _rowmajor(w, "w")
+    _check(qa.dtype == torch.int8 and w.dtype == torch.int8, "qa and w must be int8")
+    m, k = qa.shape
+    n = w.size(0)
+    _check(w.size(1) == k, f"Activation K ({k}) must match weight K ({w.size(1)})")
+    if out_dtype != torch.int32:
+        _check(sa.dtype == torch.float32 and sa.numel() == m, "sa must be float32 [M]")
+        _check(sw.dtype == torch.float32 and sw.numel() == n, "sw must be float32 [N]")
+        sa, sw = sa.contiguous(), sw.contiguous()
+    out = torch.empty((m, n), dtype=out_dtype, device=qa.device)
+    _lib.call("strix_w8a8_int8_gemm", _ptr(qa), qa.stride(0), _ptr(sa), _ptr(w), w.stride(0), _ptr(sw), _ptr(out),
+              n, _out_code(out_dtype), m, n, k, cfg, _stream(qa))
+    return out
+
+
+@_define("w8a8_scaled_mm(Tensor qa, Tensor sa, Tensor w, Tensor sw) -> Tensor")
+def w8a8_scaled_mm(qa, sa, w, sw):
+    return _i8_gemm(qa, sa, w, sw, torch.bfloat16, -1)
+
+
+@_fake("w8a8_scaled_mm")
+def _(qa, sa, w, sw):
+    return qa.new_empty((qa.size(0), w.size(0)), dtype=torch.bfloat16)
+
+
+@_define("w8a8_scaled_mm_cfg(Tensor qa, Tensor sa, Tensor w, Tensor sw, int cfg) -> Tensor")
+def w8a8_scaled_mm_cfg(qa, sa, w, sw, cfg):
+    return _i8_gemm(qa, sa, w, sw, torch.bfloat16, int(cfg))
+
+
+@_fake("w8a8_scaled_mm_cfg")
+def _(qa, sa, w, sw, cfg):
+    return qa.new_empty((qa.size(0), w.size(0)), dtype=torch.bfloat16)
+
+
+@_define("_w8a8_i32_acc(Tensor qa, Tensor w) -> Tensor")
+def _w8a8_i32_acc(qa, w):
+    return _i8_gemm(qa, None, w, None, torch.int32, -1)
+
+
+@_fake("_w8a8_i32_acc")
+def _(qa, w):
+    return qa.new_empty((qa.size(0), w.size(0)), dtype=torch.int32)
+
+
+# Reference schemas: csrc/torch_ops.cpp:277-282. uint8b128 weights [N, K]
+# (rows may be padded), activations quantized per (row, 128-group) in the op,
+# fp32 scales [G, N], [N, G] or [N].
+def _w8a8_wmma(in_w8, in_act, in_scale, cfg):
+    _check(in_w8.dim() == 2, f"Weights must be [N, K], got {in_w8.dim()} dims")
+    _check(in_act.dim() == 2, f"Activation must be [M, K], got {in_act.dim()} dims")
+    n, k = in_w8.shape
+    m = in_act.size(0)
+    _check(in_act.size(1) == k, f"Activation K ({in_act.size(1)}) must match weight K ({k})")
+    _check(in_w8.dtype == torch.uint8, f"Weights must be uint8 (uint8b128 layout, one byte per element), got {in_w8.dtype}")
+    _check(in_scale.dtype == torch.float32, f"Scale must be float32, got {in_scale.dtype}")
+    _check(k % 128 == 0, f"K must be divisible by the weight group 128, got K={k}")
+    _check(in_w8.stride(1) == 1, "Weights must be contiguous in dim 1")
+    g = k // 128
+    if in_scale.dim() == 1:
+        _check(in_scale.numel() == n and in_scale.stride(0) == 1, f"Per-channel scale must be [N={n}] contiguous")
+        ns, gs = 1, 0
+    else:
+        _check(in_scale.dim() == 2 and in_scale.stride(1) == 1, "Scale must be [G, N], [N, G] or [N]")
+        if tuple(in_scale.shape) == (g, n):
+            ns, gs = 1, in_scale.stride(0)
+        else:
+            _check(tuple(in_scale.shape) == (n, g),
+                   f"Scale must be [G, N] = [{g}, {n}], [N, G] or [N={n}] but got {list(in_scale.shape)}")
+            ns, gs = in_scale.stride(0), 1
+    x = in_act.contiguous()
+    out = torch.empty((m, n), dtype=in_act.dtype, device=in_act.device)
+    if m == 0 or n == 0:
+        return out
+    q = torch.empty((m, k), dtype=torch.int8, device=in_act.device)
+    sa = torch.empty((m, g), dtype=torch.float32, device=in_act.device)
+    st = _stream(in_act)
+    _lib.call("strix_int8_quant_group128", _ptr(x), _act_code(x), k, _ptr(q), k, _ptr(sa), g, m, k, st)
+    _lib.call("strix_w8a8_int8_group_gemm", _ptr(q), k, _ptr(sa), g, _ptr(in_w8), in_w8.stride(0), 1, _ptr(in_scale),
+              ns, gs, _ptr(out), n, _act_code(out), m, n, k, cfg, st)
+    return out
+
+
+@_define("w8a8_wmma_gemm(Tensor in_w8, Tensor in_act, Tensor in_scale) -> Tensor")
+def w8a8_wmma_gemm(in_w8, in_act, in_scale):
+    return _w8a8_wmma(in_w8, in_act, in_scale, -1)
+
+
+@_fake("w8a8_wmma_gemm")
+def _(in_w8, in_act, in_scale):
+    return in_act.new_empty((in_act.size(0), in_w8.size(0)))
+
+
+@_define("w8a8_wmma_gemm_cfg(Tensor in_w8, Tensor in_act, Tensor in_scale, int cfg) -> Tensor")
+def w8a8_wmma_gemm_cfg(in_w8, in_act, in_scale, cfg):
+    return _w8a8_wmma(in_w8, in_act, in_scale, int(cfg))
+
+
+@_fake("w8a8_wmma_gemm_cfg")
+def _(in_w8, in_act, in_scale, cfg):
+    return in_act.new_empty((in_act.size(0), in_w8.size(0)))
+
+
+# ----------------------------------------------------------------- FP8-block W8A8
+def _fp8_block(qa, sa, w, sw, cfg):
+    _rowmajor(qa, "qa")
+    _rowmajor(w, "w")
+    _check(qa.dtype == torch.float8_e4m3fn and w.dtype == torch.float8_e4m3fn, "qa and w must be float8_e4m3fn")
+    m, k = qa.shape
+    n = w.size(0)
+    _check(w.size(1) == k, f"Activation K ({k}) must match weight K ({w.size(1)})")
+    _check(k % 128 == 0, f"K must be a multiple of 128, got K={k}")
+    _check(sa.dtype == torch.float32 and tuple(sa.shape) == (m, k // 128) and sa.stride(1) == 1,
+           "sa must be float32 [M, K/128]")
+    _check(sw.dtype == torch.float32 and tuple(sw.shape) == ((n + 127) // 128, k // 128) and sw.stride(1) == 1,
+           "sw must be float32 [ceil(N/128), K/128]")
+    out = torch.empty((m, n), dtype=torch.bfloat16, device=qa.device)
+    _lib.call("strix_fp8_w8a8_block_gemm", _ptr(qa), qa.stride(0), _ptr(sa), sa.stride(0), _ptr(w), w.stride(0),
+              _ptr(sw), sw.stride(0), _ptr(out), n, _lib.BF16, m, n, k, cfg, _stream(qa))
+    return out
+
+
+@_define("fp8_w8a8_block_gemm(Tensor qa, Tensor sa, Tensor w, Tensor sw) -> Tensor")
+def fp8_w8a8_block_gemm(qa, sa, w, sw):
+    return _fp8_block(qa, sa, w, sw, -1)
+
+
+@_fake("fp8_w8a8_block_gemm")
+def _(qa, sa, w, sw):
+    return qa.new_empty((qa.size(0), w.size(0)), dtype=torch.bfloat16)
+
+
+@_define("fp8_w8a8_block_gemm_cfg(Tensor qa, Tensor sa, Tensor w, Tensor sw, int cfg) -> Tensor")
+def fp8_w8a8_block_gemm_cfg(qa, sa, w, sw, cfg):
+    return _fp8_block(qa, sa, w, sw, int(cfg))
+
+
+@_fake("fp8_w8a8_block_gemm_cfg")
+def _(qa, sa, w, sw, cfg):
+    return qa.new_empty((qa.size(0), w.size(0)), dtype=torch.bfloat16)
+
+
+# ----------------------------------------------------------------- MoE
+def _moe_common(c, sorted_ids, expert_ids, num_post_padded, topk_weights, block_m):
+    _check(sorted_ids.dtype == torch.int32 and expert_ids.dtype == torch.int32 and num_post_padded.dtype == torch.int32,
+           "sorted_ids, expert_ids and num_post_padded must be int32")
+    _check(sorted_ids.is_contiguous() and expert_ids.is_contiguous(), "routing tensors must be contiguous")
+    _check(expert_ids.numel() * block_m >= sorted_ids.numel(),
+           "expert_ids.numel() * block_m must cover sorted_ids")
+    if topk_weights is not None:
+        _check(topk_weights.dtype == torch.float32 and topk_weights.is_contiguous()
+               and topk_weights.numel() == c.size(0), "topk_weights must be float32 with one weight per slot")
+
+
+@_define(
+    "moe_gemm_fp8_w8a8(Tensor(a!) c, Tensor qa, Tensor sa, Tensor b, Tensor scales, "
+    "Tensor sorted_ids, Tensor expert_ids, Tensor num_post_padded, Tensor? topk_weights, "
+    "int top_k, int block_m, int block_n, bool silu_mul=False, str activation='silu') -> ()"
+)
+def moe_gemm_fp8_w8a8(c, qa, sa, b, scales, sorted_ids, expert_ids, num_post_padded, topk_weights, top_k, block_m,
+                      block_n, silu_mul=False, activation="silu"):
+    _check(b.dim() == 3 and b.dtype == torch.float8_e4m3fn and b.stride(2) == 1, "b must be float8_e4m3fn [E, N, K]")
+    e, n, k = b.shape
+    _rowmajor(qa, "qa")
+    _check(qa.dtype == torch.float8_e4m3fn and qa.size(1) == k, "qa must be float8_e4m3fn [rows, K]")
+    _check(sa.dtype == torch.float32 and sa.dim() == 2 and sa.size(1) == k // 128 and sa.stride(1) == 1,
+           "sa must be float32 [rows, K/128]")
+    _check(scales.dtype == torch.float32 and tuple(scales.shape) == (e, (n + 127) // 128, k // 128)
+           and scales.stride(2) == 1, "scales must be float32 [E, N/128, K/128]")
+    _check(c.dim() == 2 and c.stride(1) == 1 and c.dtype in (torch.bfloat16, torch.float16), "c must be bf16/fp16 2-D")
+    _check(n % block_n == 0, f"N={n} is not a multiple of block_n={block_n}")
+    _moe_common(c, sorted_ids, expert_ids, num_post_padded, topk_weights, block_m)
+    _lib.call("strix_moe_gemm_fp8_w8a8", _ptr(c), c.stride(0), _out_code(c.dtype), _ptr(qa), qa.stride(0), _ptr(sa),
+              sa.stride(0), _ptr(b), b.stride(0), b.stride(1), _ptr(scales), scales.stride(0), scales.stride(1),
+              _ptr(sorted_ids), sorted_ids.numel(), _ptr(expert_ids), expert_ids.numel(), _ptr(num_post_padded),
+              _ptr(topk_weights), c.size(0), top_k, block_m, int(bool(silu_mul)), _activation(activation), n, k,
+              _stream(c))
+
+
+@_fake("moe_gemm_fp8_w8a8")
+def _(c, qa, sa, b, scales, sorted_ids, expert_ids, num_post_padded, topk_weights, top_k, block_m, block_n,
+      silu_mul=False, activation="silu"):
+    return None
+
+
+@_define("moe_route_topk(Tensor logits, int top_k, bool renormalize=True) -> (Tensor, Tensor)")
+def moe_route_topk(logits, top_k, renormalize=True):
+    _rowmajor(logits, "logits")
+    _check(logits.dtype in (torch.float32, torch.bfloat16), "logits must be float32 or bfloat16")
+    t, e = logits.shape
+    ids = torch.empty((t, top_k), dtype=torch.int32, device=logits.device)
+    w = torch.empty((t, top_k), dtype=torch.float32, device=logits.device)
+    code = _lib.F32 if logits.dtype == torch.float32 else _lib.BF16
+    _lib.call("strix_moe_route_topk", _ptr(logits), code, logits.stride(0), t, e, top_k, int(bool(renormalize)),
+              _ptr(ids), _ptr(w), top_k, _stream(logits))
+    return ids, w
+
+
+@_fake("moe_route_topk")
+def _(logits, top_k, renormalize=True):
+    t = logits.size(0)
+    return (logits.new_empty((t, top_k), dtype=torch.int32), logits.new_empty((t, top_k), dtype=torch.float32))
+
+
+def align_capacity(num_slots: int, num_experts: int, block_m: int) -> tuple[int, int]:
+    cap = num_slots + num_experts * (block_m - 1)
+    return cap, (cap + block_m - 1) // block_m
+
+
+@_define("moe_align(Tensor topk_ids, int num_experts, int block_m) -> (Tensor, Tensor, Tensor)")
+def moe_align(topk_ids, num_experts, block_m):
+    _check(topk_ids.dtype == torch.int32 and topk_ids.is_contiguous(), "topk_ids must be contiguous int32")
+    s = topk_ids.numel()
+    cap, nblk = align_capacity(s, num_experts, block_m)
+    dev = topk_ids.device
+    sorted_ids = torch.empty((cap,), dtype=torch.int32, device=dev)
+    expert_ids = torch.empty((nblk,), dtype=torch.int32, device=dev)
+    num_post = torch.empty((1,), dtype=torch.int32, device=dev)
+    ws_bytes = _lib.query("strix_moe_align_workspace_bytes", s, num_experts)
+    ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev)
+    _lib.call("strix_moe_align", _ptr(topk_ids), s, num_experts, block_m, _ptr(sorted_ids), cap, _ptr(expert_ids),
+              nblk, _ptr(num_post), _ptr(ws), ws_bytes, _stream(topk_ids))
+    return sorted_ids, expert_ids, num_post
+
+
+@_fake("moe_align")
+def _(topk_ids, num_experts, block_m):
+    cap, nblk = align_capacity(topk_ids.numel(), num_experts, block_m)
+    return (topk_ids.new_empty((cap,)), topk_ids.new_empty((nblk,)), topk_ids.new_empty((1,)))
+
+
+def _sum_impl(inp, weights, output):
+    _check(inp.dim() == 3 and inp.is_contiguous(), "input must be contiguous [T, top_k, H]")
+    t, k, h = inp.shape
+    _check(output.dim() == 2 and tuple(output.shape) == (t, h) and output.stride(1) == 1
+           and output.dtype == inp.dtype, "output must be [T, H] with the input dtype")
+    if weights is not None:
+        _check(weights.dtype == torch.float32 and weights.numel() == t * k, "weights must be float32 [T, top_k]")
+        weights = weights.contiguous()
+    _lib.call("strix_moe_sum", _ptr(inp), _act_code(inp), h, t, k, h, _ptr(weights), _ptr(output), output.stride(0),
+              _stream(inp))
+
+
+# Same schema as vLLM's _moe_C::moe_sum (called at python/strix_vllm/moe.py:328-330).
+@_define("moe_sum(Tensor input, Tensor(a!) output) -> ()")
+def moe_sum(inp, output):
+    _sum_impl(inp, None, output)
+
+
+@_fake("moe_sum")
+def _(inp, output):
+    return None
+
+
+@_define("moe_weighted_sum(Tensor input, Tensor weights, Tensor(a!) output) -> ()")
+def moe_weighted_sum(inp, weights, output):
+    _sum_impl(inp, weights, output)
+
+
+@_fake("moe_weighted_sum")
+def _(inp, weights, output):
+    return None
+
+
+# ----------------------------------------------------------------- probes
+@_define("_mfma_tile(Tensor a, Tensor b) -> Tensor")
+def _mfma_tile(a, b):
+    _check(a.dim() == 2 and a.shape == b.shape and a.size(0) == 16 and a.dtype == b.dtype, "a, b must be [16, K]")
+    a, b = a.contiguous(), b.contiguous()
+    kind = {torch.bfloat16: 0, torch.float8_e4m3fn: 1, torch.int8: 2}.get(a.dtype)
+    _check(kind is not None, "probe dtypes: bfloat16, float8_e4m3fn or int8")
+    d = torch.empty((16, 16), dtype=torch.int32 if kind == 2 else torch.float32, device=a.device)
+    _lib.call("strix_probe_mfma", kind, _ptr(a), _ptr(b), _ptr(d), a.size(1), _stream(a))
+    return d
+
+
+@_fake("_mfma_tile")
+def _(a, b):
+    return a.new_empty((16, 16), dtype=torch.int32 if a.dtype == torch.int8 else torch.float32)
+
+
+@_define("_g2l_probe(Tensor src) -> Tensor")
+def _g2l_probe(src):
+    _check(src.dtype == torch.uint8 and src.numel() == 1024 and src.is_contiguous(), "src must be 1024 uint8")
+    dst = torch.empty_like(src)
+    _lib.call("strix_probe_g2l", _ptr(src), _ptr(dst), _stream(src))
+    return dst
+
+
+@_fake("_g2l_probe")
+def _(src):
+    return torch.empty_like(src)

@@ -1,0 +1,80 @@
+# SPDX-License-Identifier: MIT
+"""FP8-block W8A8 dense linear against the oracle.
+
+The oracle applies the same 1x128 activation QDQ, dequantizes the weights
+with their 128x128 block scales and runs an fp32 matmul (tests/test_fp8.py's
+pattern). Bar: max relative error 1e-2 of the peak (bf16 output).
+"""
+
+import pytest
+import torch
+
+import libstrix_amd  # noqa: F401
+import oracle
+from conftest import peak_rel_err
+from libstrix_amd import workloads
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+TOL = 1e-2
+
+
+@pytest.fixture(scope="module")
+def c2_weights():
+    d = workloads.c2_fp8(seed=2, m=1)
+    return d["w"], d["sw"]
+
+
+@pytest.mark.parametrize("m", [1, 16, 256, 4096])
+def test_config2_sweep(m, c2_weights):
+    w, sw = c2_weights
+    d = workloads.c2_fp8(seed=20 + m, m=m, weights=(w, sw))
+    x = d["x"].to(DEV)
+    qa, sa = torch.ops.strix.fp8_quant_group128(x)
+    out = torch.ops.strix.fp8_w8a8_block_gemm(qa, sa, w.to(DEV), sw.to(DEV))
+    rows = torch.arange(m) if m <= 64 else torch.randperm(m, generator=torch.Generator().manual_seed(m))[:48]
+    ref = oracle.fp8_block_gemm(qa.cpu()[rows], sa.cpu()[rows], w, sw)
+    assert peak_rel_err(out.cpu()[rows], ref) <= TOL
+
+
+@pytest.mark.parametrize("m", [1, 6, 16, 17, 33, 64, 65, 129, 300])
+@pytest.mark.parametrize("n,k", [(300, 1024), (1024, 2048)])
+def test_shapes_and_ragged_n(m, n, k):
+    d = workloads.c2_fp8(seed=m, m=m, n=n, k=k)
+    qa, sa = oracle.fp8_quant_group128(d["x"])
+    out = torch.ops.strix.fp8_w8a8_block_gemm(qa.to(DEV), sa.to(DEV), d["w"].to(DEV), d["sw"].to(DEV))
+    assert peak_rel_err(out, oracle.fp8_block_gemm(qa, sa, d["w"], d["sw"])) <= TOL
+
+
+@pytest.mark.parametrize("cfg", range(7))
+def test_every_cfg(cfg):
+    d = workloads.c2_fp8(seed=cfg, m=70, n=640, k=1536)
+    qa, sa = oracle.fp8_quant_group128(d["x"])
+    out = torch.ops.strix.fp8_w8a8_block_gemm_cfg(qa.to(DEV), sa.to(DEV), d["w"].to(DEV), d["sw"].to(DEV), cfg)
+    assert peak_rel_err(out, oracle.fp8_block_gemm(qa, sa, d["w"], d["sw"])) <= TOL
+
+
+def test_padded_weight_rows():
+    d = workloads.c2_fp8(seed=5, m=40, n=512, k=1024)
+    buf = torch.zeros(512, 1024 + 128, dtype=torch.uint8)
+    buf[:, :1024] = d["w"].view(torch.uint8)
+    wv = buf.view(torch.float8_e4m3fn).to(DEV)[:, :1024]
+    qa, sa = oracle.fp8_quant_group128(d["x"])
+    out = torch.ops.strix.fp8_w8a8_block_gemm(qa.to(DEV), sa.to(DEV), wv, d["sw"].to(DEV))
+    assert peak_rel_err(out, oracle.fp8_block_gemm(qa, sa, d["w"], d["sw"])) <= TOL
+
+
+def test_one_hot_activations_read_back_the_weights():
+    d = workloads.c2_fp8(seed=6, m=1, n=256, k=256)
+    qa = torch.zeros(256, 256).to(torch.float8_e4m3fn)
+    qa[range(256), range(256)] = 1.0
+    sa = torch.ones(256, 2)
+    out = torch.ops.strix.fp8_w8a8_block_gemm(qa.to(DEV), sa.to(DEV), d["w"].to(DEV), d["sw"].to(DEV))
+    want = oracle.fp8_block_dequant(d["w"], d["sw"]).t().to(torch.bfloat16)
+    assert torch.equal(out.cpu(), want)
+
+
+def test_rejects_bad_k():
+    x = torch.zeros(4, 96, dtype=torch.float8_e4m3fn, device=DEV)
+    with pytest.raises(RuntimeError, match="K must be a multiple of 128"):
+        torch.ops.strix.fp8_w8a8_block_gemm(x, torch.ones(4, 1, device=DEV), x, torch.ones(1, 1, device=DEV))

@@ -1,0 +1,64 @@
+# SPDX-License-Identifier: MIT
+"""The MFMA fragment conventions every kernel relies on (strix_common.h), the
+gfx950 counterpart of the reference's tests/test_wmma_layout.py."""
+
+import numpy as np
+import pytest
+import torch
+
+import libstrix_amd  # noqa: F401
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _rand(shape, seed, dtype):
+    g = torch.Generator().manual_seed(seed)
+    if dtype == torch.int8:
+        return torch.randint(-128, 128, shape, generator=g, dtype=torch.int8)
+    x = torch.randn(shape, generator=g)
+    if dtype == torch.float8_e4m3fn:
+        return (x * 8).clamp(-448, 448).to(dtype)
+    return x.to(dtype)
+
+
+@pytest.mark.parametrize("k", [32, 64, 512])
+def test_bf16_tile_matches_matmul(k):
+    a, b = _rand((16, k), 0, torch.bfloat16), _rand((16, k), 1, torch.bfloat16)
+    d = torch.ops.strix._mfma_tile(a.to(DEV), b.to(DEV)).cpu()
+    torch.testing.assert_close(d, a.float() @ b.float().t(), rtol=1e-5, atol=1e-4)
+
+
+@pytest.mark.parametrize("k", [128, 512])
+def test_fp8_tile_matches_matmul(k):
+    a, b = _rand((16, k), 2, torch.float8_e4m3fn), _rand((16, k), 3, torch.float8_e4m3fn)
+    d = torch.ops.strix._mfma_tile(a.to(DEV), b.to(DEV)).cpu()
+    ref = (a.double() @ b.double().t()).float()
+    torch.testing.assert_close(d, ref, rtol=1e-5, atol=1e-3)
+
+
+@pytest.mark.parametrize("k", [64, 512])
+def test_int8_tile_is_exact(k):
+    a, b = _rand((16, k), 4, torch.int8), _rand((16, k), 5, torch.int8)
+    d = torch.ops.strix._mfma_tile(a.to(DEV), b.to(DEV)).cpu().numpy()
+    assert np.array_equal(d, a.numpy().astype(np.int64) @ b.numpy().astype(np.int64).T)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float8_e4m3fn, torch.int8])
+def test_layout_is_not_transposed(dtype):
+    k = {torch.bfloat16: 32, torch.float8_e4m3fn: 128, torch.int8: 64}[dtype]
+    a = torch.zeros(16, k)
+    b = torch.zeros(16, k)
+    a[3, 5] = 1
+    b[11, 5] = 2
+    a[7, k - 1] = 1  # the last K position of a lane group lands too
+    b[2, k - 1] = 1
+    d = torch.ops.strix._mfma_tile(a.to(dtype).to(DEV), b.to(dtype).to(DEV)).cpu()
+    assert d[3, 11] == 2 and d[7, 2] == 1 and d.count_nonzero() == 2
+
+
+def test_global_to_lds_lane_placement():
+    src = torch.arange(1024, dtype=torch.int64).to(torch.uint8)
+    dst = torch.ops.strix._g2l_probe(src.to(DEV)).cpu()
+    want = src.reshape(64, 16).flip(0).reshape(-1)
+    assert torch.equal(dst, want)

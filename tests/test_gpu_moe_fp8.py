@@ -1,0 +1,133 @@
+# SPDX-License-Identifier: MIT
+"""MoE plumbing and the FP8-block W8A8 fused MoE.
+
+Routing ids, sorted ids, expert ids and num_post_padded are compared bit for
+bit; floating outputs within max relative error 1e-2 of the peak. Outputs
+start as NaN so an unwritten slot fails (tests/test_moe_gemm.py:68-70).
+"""
+
+import pytest
+import torch
+
+import libstrix_amd  # noqa: F401
+import oracle
+from conftest import peak_rel_err
+from libstrix_amd import functional, workloads
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+TOL = 1e-2
+
+
+@pytest.mark.parametrize("t,e,k", [(4096, 128, 8), (2048, 32, 4), (1, 128, 8), (7, 1000, 5)])
+@pytest.mark.parametrize("renorm", [True, False])
+def test_route_ids_bit_exact(t, e, k, renorm):
+    logits = torch.randn(t, e, generator=torch.Generator().manual_seed(t + e))
+    ids, w = torch.ops.strix.moe_route_topk(logits.to(DEV), k, renorm)
+    rid, rw = oracle.route_topk(logits, k, renorm)
+    assert torch.equal(ids.cpu(), rid)
+    torch.testing.assert_close(w.cpu(), rw, rtol=1e-5, atol=1e-7)
+
+
+def test_route_ties_and_bf16_logits():
+    logits = torch.zeros(3, 64)
+    logits[0, [5, 9, 40]] = 1.0       # a three-way tie: lower ids first
+    logits[1, :] = 0.5                # all equal: ids 0..k-1
+    logits[2, [63, 0]] = 2.0
+    lb = logits.to(torch.bfloat16)
+    ids, _ = torch.ops.strix.moe_route_topk(lb.to(DEV), 4, True)
+    rid, _ = oracle.route_topk(lb.float(), 4, True)
+    assert torch.equal(ids.cpu(), rid)
+    assert ids.cpu()[0].tolist()[:3] == [5, 9, 40] and ids.cpu()[1].tolist() == [0, 1, 2, 3]
+
+
+@pytest.mark.parametrize("t,k,e,bm", [(1, 8, 128, 16), (64, 8, 128, 16), (5, 4, 16, 32), (2048, 4, 32, 64),
+                                      (4096, 8, 128, 128), (8192, 8, 128, 256), (300, 8, 256, 64)])
+def test_align_bit_exact(t, k, e, bm):
+    g = torch.Generator().manual_seed(t * 7 + e)
+    ids = torch.stack([torch.randperm(e, generator=g)[:k] for _ in range(t)]).to(torch.int32)
+    sorted_ids, expert_ids, num_post = torch.ops.strix.moe_align(ids.to(DEV), e, bm)
+    rs, re, total = oracle.align(ids, bm, e)
+    assert int(num_post.item()) == total
+    s = sorted_ids.cpu()
+    assert s[:total].tolist() == rs
+    assert (s[total:] == t * k).all()
+    x = expert_ids.cpu()
+    assert x[:total // bm].tolist() == re
+    assert (x[total // bm:] == -1).all()
+
+
+def test_moe_sum_bit_exact():
+    y = torch.randn(37, 8, 2048, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16)
+    out = torch.empty(37, 2048, dtype=torch.bfloat16, device=DEV)
+    torch.ops.strix.moe_sum(y.to(DEV), out)
+    assert torch.equal(out.cpu(), oracle.moe_sum(y.reshape(-1, 2048), 8).to(torch.bfloat16))
+
+
+# ---------------------------------------------------------------- expert GEMM
+E_SMALL, TOPK = 16, 8
+
+
+@pytest.fixture(scope="module")
+def small_experts():
+    d = workloads.c3_fp8_moe(seed=11, t=1, e=E_SMALL)
+    deq13 = torch.stack([oracle.fp8_block_dequant(d["w13"][i], d["w13_s"][i]) for i in range(E_SMALL)])
+    deq2 = torch.stack([oracle.fp8_block_dequant(d["w2"][i], d["w2_s"][i]) for i in range(E_SMALL)])
+    return d, deq13, deq2
+
+
+@pytest.mark.parametrize("tokens", [1, 5, 40, 300])
+@pytest.mark.parametrize("block_m", [16, 32, 64, 128, 256])
+@pytest.mark.parametrize("gemm,activation", [("w13", "silu"), ("w13", "gelu_tanh"), ("w2", "silu")])
+def test_expert_gemm(tokens, block_m, gemm, activation, small_experts):
+    d, deq13, deq2 = small_experts
+    g = torch.Generator().manual_seed(tokens * 31 + block_m)
+    ids = torch.stack([torch.randperm(E_SMALL, generator=g)[:TOPK] for _ in range(tokens)]).to(torch.int32)
+    if gemm == "w13":
+        w, ws, deq, k_in = d["w13"], d["w13_s"], deq13, 2048
+        a = torch.randn(tokens, k_in, generator=g).to(torch.bfloat16)
+        a_topk, weights, cols = TOPK, None, deq.size(1) // 2
+    else:
+        w, ws, deq, k_in = d["w2"], d["w2_s"], deq2, 768
+        a = torch.randn(tokens * TOPK, k_in, generator=g).to(torch.bfloat16)
+        a_topk, weights, cols = 1, torch.rand(tokens, TOPK, generator=g), deq.size(1)
+    qa, sa = oracle.fp8_quant_group128(a)
+    sorted_ids, expert_ids, num_post = torch.ops.strix.moe_align(ids.to(DEV), E_SMALL, block_m)
+    c = torch.full((tokens * TOPK, cols), float("nan"), dtype=torch.bfloat16, device=DEV)
+    torch.ops.strix.moe_gemm_fp8_w8a8(c, qa.to(DEV), sa.to(DEV), w.to(DEV), ws.to(DEV), sorted_ids, expert_ids,
+                                      num_post, None if weights is None else weights.reshape(-1).to(DEV), a_topk,
+                                      block_m, 128, gemm == "w13", activation)
+    a_deq = qa.float() * sa.repeat_interleave(128, dim=1)
+    ref = oracle.moe_expert_gemm(a_deq, deq, ids, a_topk, weights)
+    if gemm == "w13":
+        n2 = cols
+        g_, u_ = ref[:, :n2], ref[:, n2:]
+        act = torch.nn.functional.silu(g_) if activation == "silu" else torch.nn.functional.gelu(g_, approximate="tanh")
+        ref = act * u_
+    assert not torch.isnan(c).any()
+    assert peak_rel_err(c, ref) <= TOL
+
+
+# ---------------------------------------------------------------- fused, config 3
+@pytest.fixture(scope="module")
+def c3_weights():
+    d = workloads.c3_fp8_moe(seed=3, t=1)
+    dev = {k: (v.to(DEV) if isinstance(v, torch.Tensor) else v) for k, v in d.items()}
+    return d, dev
+
+
+@pytest.mark.parametrize("t", [1, 64, 4096])
+def test_config3_fused_moe(t, c3_weights):
+    d, dev = c3_weights
+    g = torch.Generator().manual_seed(100 + t)
+    x = torch.randn(t, 2048, generator=g).to(torch.bfloat16)
+    logits = torch.randn(t, 128, generator=g)
+    out = functional.fused_moe_fp8_w8a8(x.to(DEV), logits.to(DEV), dev["w13"], dev["w13_s"], dev["w2"],
+                                        dev["w2_s"], 8)
+    ids, w = oracle.route_topk(logits, 8)
+    rows = list(range(t)) if t <= 64 else torch.randperm(t, generator=g)[:32].tolist()
+    ref = oracle.fused_moe(x, ids, w,
+                           lambda e: oracle.fp8_block_dequant(d["w13"][e], d["w13_s"][e]),
+                           lambda e: oracle.fp8_block_dequant(d["w2"][e], d["w2_s"][e]),
+                           act_quant="fp8", tokens=rows)
+    assert peak_rel_err(out.cpu()[rows], ref) <= TOL
