@@ -37,6 +37,10 @@ HIPCC_FLAGS = [
     "-target-feature",
     "-Xclang",
     "-packed-fp32-ops",
+    # MFMA results in arch VGPRs: the block-scale fold reads every result
+    # with a VALU FMA, which cannot take AGPR operands.
+    "-mllvm",
+    "-amdgpu-mfma-vgpr-form",
     "-Wno-unused-command-line-argument",
 ]
 

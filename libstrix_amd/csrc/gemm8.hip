@@ -49,7 +49,6 @@ struct G8 {
   const int32_t* num_post;
   int num_slots, top_k;
   const float* topk_w;
-  int w_excess128;   // weights stored as uint8b128 (byte - 128)
 };
 
 __device__ __forceinline__ u32x4 ldg128(const uint8_t* p) {
@@ -158,11 +157,12 @@ __device__ __forceinline__ void finish4(const G8& p, int orow, int brow, bool va
 }
 
 // ============================================================ stream8
-template <int KIND, int NT, int MT, int WAVES, bool MOE, int EPI, int ACT, int U>
+template <int KIND, int NT, int MT, int WAVES, bool MOE, int EPI, int ACT, int U, bool WX128>
 __global__ void __launch_bounds__(WAVES * 64) stream8_kernel(G8 p) {
   constexpr int NTH = (EPI == kEpiGated) ? NT / 2 : NT;  // output subtiles
   constexpr bool INT_ACC = (KIND == kI8Token);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r16 = lane & 15, g4 = lane >> 4;
   const int m0 = blockIdx.y * (16 * MT);
   int expert = 0;
@@ -267,7 +267,7 @@ __global__ void __launch_bounds__(WAVES * 64) stream8_kernel(G8 p) {
 #pragma unroll
     for (int s = 0; s < NT; ++s) {
       af[s] = cat8(ldg128(wp[s] + ko), ldg128(wp[s] + ko + 64));
-      if (p.w_excess128) af[s] = flip80(af[s]);
+      if constexpr (WX128) af[s] = flip80(af[s]);
     }
 #pragma unroll
     for (int t = 0; t < MT; ++t) bf[t] = cat8(ldg128(ap[t] + ko), ldg128(ap[t] + ko + 64));
@@ -336,29 +336,56 @@ __global__ void __launch_bounds__(WAVES * 64) stream8_kernel(G8 p) {
 }
 
 // ============================================================ tiled8
-// Fragment-native LDS stage: region q = 2*subtile + half holds, at byte
-// 16*l, the 16 bytes that lane l feeds the MFMA for that (subtile, half).
-// Subtiles 0..SA-1 are weight rows, SA..SA+SB-1 token rows; after them the
-// stage keeps BM fp32 activation scales.
-template <int KIND, int BM, int BN, int WM, int WN, bool MOE, int EPI, int ACT>
+// LDS stage: operand rows of 128 bytes (the stage's 128-K block), weight
+// rows 0..BN-1 then token rows, each row's 16-byte chunks XOR-swizzled
+// (lds_swz). Subtile j = 16 consecutive rows = 2 KiB. After them each
+// stage keeps the scales of its 128-K block: BM activation scales, then the
+// weight scales (fp8: one per weight subtile; int8 group: one per weight row).
+// Every byte of a stage, scales included, arrives by direct global->LDS copy,
+// so a wave's outstanding copies retire strictly in issue order and
+// `s_waitcnt vmcnt(n)` with n = copies issued for later stages waits for
+// exactly one stage.
+// LDS row swizzle: chunk c of operand row r sits at slot c ^ lds_swz(r), so
+// the 16 lanes of a ds_read_b128 group (rows r..r+15, one chunk index) hit 16
+// distinct 16-byte bank groups.
+__device__ __forceinline__ int lds_swz(int row) { return (row >> 1) & 7; }
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit counter");
+  // gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+template <int KIND, int BM, int BN, int WM, int WN, int STAGES, bool MOE, int EPI, int ACT, bool WX128>
 __global__ void __launch_bounds__(WM * WN * 64) tiled8_kernel(G8 p, int tiles_m, int tiles_n, int group_m) {
   constexpr int W = WM * WN;
   constexpr int TM = BM / WM, TN = BN / WN;
   constexpr int MT = TM / 16, NT = TN / 16;
   constexpr int SA = BN / 16, SB = BM / 16;
-  constexpr int NQ = 2 * (SA + SB);              // 1 KiB copies per stage
-  constexpr int QPW = (NQ + W - 1) / W;          // copies per wave
+  constexpr int NQ = 2 * (SA + SB);  // 1 KiB operand copies per stage (8 rows each)
+  static_assert(NQ % W == 0, "operand copies split evenly over the waves");
+  constexpr int QPW = NQ / W;
   constexpr bool HAS_SA = (KIND != kI8Token);
-  constexpr int SA_BYTES = HAS_SA ? BM * 4 : 0;
-  constexpr int STAGE = NQ * 1024 + SA_BYTES;
+  constexpr int SA_COPIES = HAS_SA ? BM / 64 : 0;
+  constexpr int SW_COPIES = (KIND == kFp8Block) ? 1 : (KIND == kI8Group ? BN / 64 : 0);
+  constexpr int EXTRA = SA_COPIES + SW_COPIES;  // wave w < EXTRA issues one more copy
+  static_assert(EXTRA <= W, "at most one scale copy per wave");
+  static_assert(!HAS_SA || BM % 64 == 0, "scale copies move 64 rows");
+  static_assert(KIND != kI8Group || BN % 64 == 0, "int8 group weight scales move 64 rows");
+  constexpr int SA_OFF = NQ * 1024;
+  constexpr int SW_OFF = SA_OFF + (HAS_SA ? BM * 4 : 0);
+  constexpr int STAGE = SW_OFF + (KIND == kFp8Block ? 256 : (KIND == kI8Group ? BN * 4 : 0));
   constexpr bool GATED = (EPI == kEpiGated);
   constexpr int NTH = GATED ? NT / 2 : NT;
   constexpr bool INT_ACC = (KIND == kI8Token);
-  static_assert(BM % 64 == 0 || !HAS_SA, "scale staging uses 64-row copies");
+  // One weight-scale value per wave and K block when the wave's rows sit in one 128-row block.
+  constexpr bool ONE_SW = !GATED && TN <= 128 && (128 % TN == 0);
   static_assert(!GATED || (NT % 2 == 0), "gated wave tiles pair gate and up subtiles");
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * STAGE];
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r16 = lane & 15, g4 = lane >> 4;
   const int wm = wave % WM, wn = wave / WM;
 
@@ -384,8 +411,7 @@ __global__ void __launch_bounds__(WM * WN * 64) tiled8_kernel(G8 p, int tiles_m,
     tn = in / gm;
   }
   const int m0 = tm * BM;
-  // Weight row of LDS weight subtile j.
-  auto wrow_of = [&](int j) -> int {
+  auto wrow_of = [&](int j) -> int {  // first weight row of LDS weight subtile j
     if constexpr (GATED) {
       const int base = tn * (BN / 2);
       return j < SA / 2 ? base + 16 * j : p.gate_off + base + 16 * (j - SA / 2);
@@ -394,61 +420,80 @@ __global__ void __launch_bounds__(WM * WN * 64) tiled8_kernel(G8 p, int tiles_m,
     }
   };
 
-  // Per-wave copy slots: fixed global row pointers, advanced 128 B per stage.
+  // Copy slots: a uniform base pointer plus a fixed 32-bit per-lane offset.
+  // Copy q moves 8 operand rows x 128 contiguous bytes (8 whole cache
+  // lines): lane l takes row 8q + l/8 and stores to LDS slot l%8 the 16-byte
+  // chunk (l%8) ^ swz(row) of that row.
   const uint8_t* wbase = p.w + (int64_t)expert * p.w_es;
-  const uint8_t* qptr[QPW];
+  uint32_t qoff[QPW];
+  bool qis_w[QPW];
 #pragma unroll
   for (int j = 0; j < QPW; ++j) {
     const int q = wave + W * j;
-    const int sub = q >> 1, half = q & 1;
-    const uint8_t* ptr = nullptr;
-    if (q < NQ) {
-      if (sub < SA) {
-        const int r = min(wrow_of(sub) + r16, p.N - 1);
-        ptr = wbase + (int64_t)r * p.ldw;
-      } else {
-        int br, orw;
-        bool v;
-        token_row<MOE>(p, m0 + 16 * (sub - SA) + r16, br, orw, v);
-        ptr = p.a + (int64_t)br * p.lda;
-      }
-      ptr += 64 * half + 16 * g4;
+    const int row = 8 * q + (lane >> 3);  // operand row: weights first, then tokens
+    uint32_t off;
+    if (row < BN) {
+      const int r = min(wrow_of(row >> 4) + (row & 15), p.N - 1);
+      off = (uint32_t)r * (uint32_t)p.ldw;
+      qis_w[j] = true;
+    } else {
+      int br, orw;
+      bool v;
+      token_row<MOE>(p, m0 + (row - BN), br, orw, v);
+      off = (uint32_t)br * (uint32_t)p.lda;
+      qis_w[j] = false;
     }
-    qptr[j] = ptr;
+    qoff[j] = off + 16 * ((lane & 7) ^ lds_swz(row));
   }
-  const float* saptr = nullptr;  // scale copy slot: wave w < BM/64 copies rows 64w..64w+63
-  if constexpr (HAS_SA) {
-    if (wave < BM / 64) {
+  // Fragment reads: lane l reads row 16*subtile + l%16, chunks l/16 (half 0)
+  // and 4 + l/16 (half 1), at their swizzled slots.
+  const uint32_t frag0 = (uint32_t)r16 * 128 + 16 * ((g4) ^ lds_swz(r16));
+  const uint32_t frag1 = (uint32_t)r16 * 128 + 16 * ((4 + g4) ^ lds_swz(r16));
+  // Scale copy slot of this wave (if any): a per-lane pointer advanced by K block.
+  const float* xptr = nullptr;
+  int64_t xstride = 0;
+  const bool has_extra = wave < EXTRA;
+  if (has_extra) {
+    if (wave < SA_COPIES) {
       int br, orw;
       bool v;
       token_row<MOE>(p, m0 + 64 * wave + lane, br, orw, v);
-      saptr = p.sa + (int64_t)br * p.sa_rs;
+      xptr = p.sa + (int64_t)br * p.sa_rs;
+      xstride = p.sa_ks;
+    } else if constexpr (KIND == kFp8Block) {
+      const int j = lane < SA ? lane : 0;
+      xptr = p.sw + (int64_t)expert * p.sw_es + (int64_t)(wrow_of(j) >> 7) * p.sw_ns;
+      xstride = p.sw_ks;
+    } else if constexpr (KIND == kI8Group) {
+      const int r = 64 * (wave - SA_COPIES) + lane;  // weight row within the block
+      const int row = min(wrow_of(r >> 4) + (r & 15), p.N - 1);
+      xptr = p.sw + (int64_t)expert * p.sw_es + (int64_t)row * p.sw_ns;
+      xstride = p.sw_ks;
     }
   }
 
   auto issue = [&](int kb, int buf) {
     uint8_t* st = smem + buf * STAGE;
+    const int64_t ko = (int64_t)kb * 128;
 #pragma unroll
     for (int j = 0; j < QPW; ++j) {
-      const int q = wave + W * j;
-      if (q < NQ) g2l_b128(qptr[j] + (int64_t)kb * 128, st + q * 1024);
+      const uint8_t* base = qis_w[j] ? wbase : p.a;
+      g2l_b128(base + ko + qoff[j], st + (wave + W * j) * 1024);
     }
-    if constexpr (HAS_SA) {
-      if (wave < BM / 64) g2l_b32(saptr + (int64_t)kb * p.sa_ks, st + NQ * 1024 + wave * 256);
+    if (has_extra) {
+      uint8_t* dst = wave < SA_COPIES ? st + SA_OFF + wave * 256 : st + SW_OFF + (wave - SA_COPIES) * 256;
+      g2l_b32(xptr + (int64_t)kb * xstride, dst);
     }
   };
 
-  // Wave's A subtiles (LDS indices) and their first weight rows.
-  int aidx[NT], arow0[NT];
+  int aidx[NT];
 #pragma unroll
   for (int s = 0; s < NT; ++s) {
     if constexpr (GATED)
       aidx[s] = s < NTH ? wn * NTH + s : SA / 2 + wn * NTH + (s - NTH);
     else
       aidx[s] = wn * NT + s;
-    arow0[s] = wrow_of(aidx[s]);
   }
-  const float* swb = p.sw + (int64_t)expert * p.sw_es;
 
   v4f acc[NT][MT];
   v4i acci[NT][MT];
@@ -461,36 +506,53 @@ __global__ void __launch_bounds__(WM * WN * 64) tiled8_kernel(G8 p, int tiles_m,
     }
 
   const int nkb = p.K >> 7;
-  issue(0, 0);
+#pragma unroll
+  for (int s0 = 0; s0 < STAGES - 1; ++s0)
+    if (s0 < nkb) issue(s0, s0);
+
   for (int kb = 0; kb < nkb; ++kb) {
-    const int buf = kb & 1;
-    wait_vmem();
-    __syncthreads();
-    if (kb + 1 < nkb) issue(kb + 1, buf ^ 1);
+    const int buf = kb % STAGES;
+    // Copies issued after stage kb: STAGES-2 stages in steady state.
+    constexpr int AHEAD = STAGES - 2;
+    if (kb + AHEAD <= nkb - 1) {
+      if (has_extra) wait_vmcnt<AHEAD * (QPW + 1)>(); else wait_vmcnt<AHEAD * QPW>();
+    } else {
+      wait_vmcnt<0>();
+    }
+    lds_barrier();
+    if (kb + STAGES - 1 < nkb) issue(kb + STAGES - 1, (kb + STAGES - 1) % STAGES);
+
     const uint8_t* st = smem + buf * STAGE;
     v8i bf[MT];
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
-      const int q = 2 * (SA + wm * MT + t);
-      bf[t] = cat8(lds128(st + q * 1024 + 16 * lane), lds128(st + (q + 1) * 1024 + 16 * lane));
+      const uint8_t* sub = st + (SA + wm * MT + t) * 2048;
+      bf[t] = cat8(lds128(sub + frag0), lds128(sub + frag1));
     }
     float sa_t[MT];
     if constexpr (HAS_SA) {
-      const float* sl = reinterpret_cast<const float*>(st + NQ * 1024);
+      const float* sl = reinterpret_cast<const float*>(st + SA_OFF);
 #pragma unroll
       for (int t = 0; t < MT; ++t) sa_t[t] = sl[wm * TM + 16 * t + r16];
     }
+    const float* swl = reinterpret_cast<const float*>(st + SW_OFF);
+    float c1[MT];
+    if constexpr (KIND == kFp8Block && ONE_SW) {
+      const float sw = swl[aidx[0]];
+#pragma unroll
+      for (int t = 0; t < MT; ++t) c1[t] = sw * sa_t[t];
+    }
 #pragma unroll
     for (int s = 0; s < NT; ++s) {
-      const int q = 2 * aidx[s];
-      v8i af = cat8(lds128(st + q * 1024 + 16 * lane), lds128(st + (q + 1) * 1024 + 16 * lane));
-      if (p.w_excess128) af = flip80(af);
+      const uint8_t* sub = st + aidx[s] * 2048;
+      v8i af = cat8(lds128(sub + frag0), lds128(sub + frag1));
+      if constexpr (WX128) af = flip80(af);
       if constexpr (KIND == kFp8Block) {
-        const float sw = swb[(int64_t)(arow0[s] >> 7) * p.sw_ns + (int64_t)kb * p.sw_ks];
+        const float sw = ONE_SW ? 0.f : swl[aidx[s]];
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
           const v4f part = mfma_fp8(af, bf[t], v4f{0.f, 0.f, 0.f, 0.f});
-          const float c = sw * sa_t[t];
+          const float c = ONE_SW ? c1[t] : sw * sa_t[t];
 #pragma unroll
           for (int i = 0; i < 4; ++i) acc[s][t][i] = fmaf(part[i], c, acc[s][t][i]);
         }
@@ -503,10 +565,7 @@ __global__ void __launch_bounds__(WM * WN * 64) tiled8_kernel(G8 p, int tiles_m,
       } else {
         float sw4[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int n = min(arow0[s] + 4 * g4 + i, p.N - 1);
-          sw4[i] = swb[(int64_t)n * p.sw_ns + (int64_t)kb * p.sw_ks];
-        }
+        for (int i = 0; i < 4; ++i) sw4[i] = swl[16 * aidx[s] + 4 * g4 + i];
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
           v4i part = mfma_i8(lo4(af), lo4(bf[t]), v4i{0, 0, 0, 0});
@@ -541,49 +600,52 @@ __global__ void __launch_bounds__(WM * WN * 64) tiled8_kernel(G8 p, int tiles_m,
 }
 
 // ============================================================ launchers
-template <int KIND, int NT, int MT, int WAVES, bool MOE, int EPI, int ACT, int U>
+template <int KIND, int NT, int MT, int WAVES, bool MOE, int EPI, int ACT, int U, bool WX128>
 int launch_stream(const G8& p, int grid_y, hipStream_t st, const char* op) {
   constexpr int NTH = (EPI == kEpiGated) ? NT / 2 : NT;
   const int grid_x = (p.n_out + 16 * NTH - 1) / (16 * NTH);
-  hipLaunchKernelGGL((stream8_kernel<KIND, NT, MT, WAVES, MOE, EPI, ACT, U>), dim3(grid_x, grid_y),
+  hipLaunchKernelGGL((stream8_kernel<KIND, NT, MT, WAVES, MOE, EPI, ACT, U, WX128>), dim3(grid_x, grid_y),
                      dim3(WAVES * 64), 0, st, p);
   return check_launch(op);
 }
 
-template <int KIND, int BM, int BN, int WM, int WN, bool MOE, int EPI, int ACT>
+template <int KIND, int BM, int BN, int WM, int WN, int STAGES, bool MOE, int EPI, int ACT, bool WX128>
 int launch_tiled(const G8& p, int grid_y_moe, hipStream_t st, const char* op) {
   constexpr int COLS = (EPI == kEpiGated) ? BN / 2 : BN;
   const int tiles_n = (p.n_out + COLS - 1) / COLS;
   if constexpr (MOE) {
-    hipLaunchKernelGGL((tiled8_kernel<KIND, BM, BN, WM, WN, MOE, EPI, ACT>), dim3(tiles_n, grid_y_moe),
-                       dim3(WM * WN * 64), 0, st, p, 0, tiles_n, 0);
+    hipLaunchKernelGGL((tiled8_kernel<KIND, BM, BN, WM, WN, STAGES, MOE, EPI, ACT, WX128>),
+                       dim3(tiles_n, grid_y_moe), dim3(WM * WN * 64), 0, st, p, 0, tiles_n, 0);
   } else {
     const int tiles_m = (p.M + BM - 1) / BM;
-    hipLaunchKernelGGL((tiled8_kernel<KIND, BM, BN, WM, WN, MOE, EPI, ACT>), dim3(tiles_m * tiles_n),
-                       dim3(WM * WN * 64), 0, st, p, tiles_m, tiles_n, 8);
+    hipLaunchKernelGGL((tiled8_kernel<KIND, BM, BN, WM, WN, STAGES, MOE, EPI, ACT, WX128>),
+                       dim3(tiles_m * tiles_n), dim3(WM * WN * 64), 0, st, p, tiles_m, tiles_n, 8);
   }
   return check_launch(op);
 }
 
 // Dense dispatch by M. cfg >= 0 pins one tile config (tile sweeps).
-template <int KIND, int EPI>
+template <int KIND, int EPI, bool WX128>
 int dense_dispatch(const G8& p, hipStream_t st, const char* op, int cfg) {
   const int M = p.M;
   if (cfg < 0) {
     if (M <= 16) cfg = 0;
     else if (M <= 32) cfg = 1;
     else if (M <= 64) cfg = 2;
-    else if (M <= 256) cfg = 4;
+    else if (M <= 512) cfg = 3;
     else cfg = 5;
   }
   switch (cfg) {
-    case 0: return launch_stream<KIND, 1, 1, 8, false, EPI, kActSilu, 4>(p, (M + 15) / 16, st, op);
-    case 1: return launch_stream<KIND, 1, 2, 8, false, EPI, kActSilu, 4>(p, (M + 31) / 32, st, op);
-    case 2: return launch_stream<KIND, 1, 4, 4, false, EPI, kActSilu, 2>(p, (M + 63) / 64, st, op);
-    case 3: return launch_tiled<KIND, 128, 128, 2, 2, false, EPI, kActSilu>(p, 0, st, op);
-    case 4: return launch_tiled<KIND, 256, 64, 4, 2, false, EPI, kActSilu>(p, 0, st, op);
-    case 5: return launch_tiled<KIND, 256, 256, 4, 2, false, EPI, kActSilu>(p, 0, st, op);
-    case 6: return launch_tiled<KIND, 128, 256, 2, 2, false, EPI, kActSilu>(p, 0, st, op);
+    case 0: return launch_stream<KIND, 1, 1, 8, false, EPI, kActSilu, 4, WX128>(p, (M + 15) / 16, st, op);
+    case 1: return launch_stream<KIND, 1, 2, 8, false, EPI, kActSilu, 4, WX128>(p, (M + 31) / 32, st, op);
+    case 2: return launch_stream<KIND, 1, 4, 4, false, EPI, kActSilu, 2, WX128>(p, (M + 63) / 64, st, op);
+    case 3: return launch_tiled<KIND, 128, 128, 2, 2, 4, false, EPI, kActSilu, WX128>(p, 0, st, op);
+    case 4: return launch_tiled<KIND, 256, 64, 4, 2, 3, false, EPI, kActSilu, WX128>(p, 0, st, op);
+    case 5: return launch_tiled<KIND, 256, 256, 4, 2, 2, false, EPI, kActSilu, WX128>(p, 0, st, op);
+    case 6:
+      // int8 group scales need one copy per 64 weight rows: 4 waves cannot carry 256 rows of them.
+      if constexpr (KIND == kI8Group) return launch_tiled<KIND, 128, 128, 2, 2, 4, false, EPI, kActSilu, WX128>(p, 0, st, op);
+      else return launch_tiled<KIND, 128, 256, 2, 2, 3, false, EPI, kActSilu, WX128>(p, 0, st, op);
     default: return set_error(STRIX_ERR_INVALID, "%s: cfg must be in 0..6, got %d", op, cfg);
   }
 }
@@ -591,12 +653,13 @@ int dense_dispatch(const G8& p, hipStream_t st, const char* op, int cfg) {
 // MoE dispatch by block_m (the sorted-id granularity).
 template <int KIND, int EPI, int ACT>
 int moe_dispatch(const G8& p, int block_m, int num_blocks, hipStream_t st, const char* op) {
+  constexpr int NTS = (EPI == kEpiGated) ? 2 : 1;
   switch (block_m) {
-    case 16: return launch_stream<KIND, (EPI == kEpiGated ? 2 : 1), 1, 4, true, EPI, ACT, 2>(p, num_blocks, st, op);
-    case 32: return launch_stream<KIND, (EPI == kEpiGated ? 2 : 1), 2, 4, true, EPI, ACT, 2>(p, num_blocks, st, op);
-    case 64: return launch_tiled<KIND, 64, 128, 1, 4, true, EPI, ACT>(p, num_blocks, st, op);
-    case 128: return launch_tiled<KIND, 128, 128, 2, 2, true, EPI, ACT>(p, num_blocks, st, op);
-    case 256: return launch_tiled<KIND, 256, 128, 4, 2, true, EPI, ACT>(p, num_blocks, st, op);
+    case 16: return launch_stream<KIND, NTS, 1, 4, true, EPI, ACT, 2, false>(p, num_blocks, st, op);
+    case 32: return launch_stream<KIND, NTS, 2, 4, true, EPI, ACT, 2, false>(p, num_blocks, st, op);
+    case 64: return launch_tiled<KIND, 64, 128, 1, 4, 4, true, EPI, ACT, false>(p, num_blocks, st, op);
+    case 128: return launch_tiled<KIND, 128, 128, 2, 2, 4, true, EPI, ACT, false>(p, num_blocks, st, op);
+    case 256: return launch_tiled<KIND, 256, 128, 4, 2, 3, true, EPI, ACT, false>(p, num_blocks, st, op);
     default: return set_error(STRIX_ERR_INVALID, "%s: block_m must be 16, 32, 64, 128 or 256, got %d", op, block_m);
   }
 }
@@ -638,7 +701,7 @@ int strix_fp8_w8a8_block_gemm(const uint8_t* qa, int64_t lda, const float* sa, i
   p.a = qa; p.lda = lda; p.sa = sa; p.sa_rs = sa_ld; p.sa_ks = 1;
   p.out = out; p.ldo = ldo; p.out_f16 = out_dtype == STRIX_F16;
   p.M = (int)M; p.N = (int)N; p.K = (int)K; p.n_out = (int)N;
-  return dense_dispatch<kFp8Block, kEpiStore>(p, as_stream(stream), op, cfg);
+  return dense_dispatch<kFp8Block, kEpiStore, false>(p, as_stream(stream), op, cfg);
 }
 
 int strix_w8a8_int8_gemm(const int8_t* qa, int64_t lda, const float* sa, const int8_t* w, int64_t ldw,
@@ -658,9 +721,9 @@ int strix_w8a8_int8_gemm(const int8_t* qa, int64_t lda, const float* sa, const i
   p.a = reinterpret_cast<const uint8_t*>(qa); p.lda = lda; p.sa = sa; p.sa_rs = 1; p.sa_ks = 0;
   p.out = out; p.ldo = ldo; p.out_f16 = out_dtype == STRIX_F16;
   p.M = (int)M; p.N = (int)N; p.K = (int)K; p.n_out = (int)N;
-  if (out_dtype == STRIX_I32) return dense_dispatch<kI8Token, kEpiI32>(p, as_stream(stream), op, cfg);
+  if (out_dtype == STRIX_I32) return dense_dispatch<kI8Token, kEpiI32, false>(p, as_stream(stream), op, cfg);
   STRIX_REQUIRE(sa != nullptr && sw != nullptr, "%s: scales are required for a float output", op);
-  return dense_dispatch<kI8Token, kEpiStore>(p, as_stream(stream), op, cfg);
+  return dense_dispatch<kI8Token, kEpiStore, false>(p, as_stream(stream), op, cfg);
 }
 
 int strix_w8a8_int8_group_gemm(const int8_t* qa, int64_t lda, const float* sa, int64_t sa_ld,
@@ -675,12 +738,13 @@ int strix_w8a8_int8_group_gemm(const int8_t* qa, int64_t lda, const float* sa, i
   if (M == 0 || N == 0) return STRIX_OK;
   STRIX_ARCH_GATE();
   G8 p = {};
-  p.w = w; p.ldw = ldw; p.w_excess128 = w_excess128;
+  p.w = w; p.ldw = ldw;
   p.sw = sw; p.sw_ns = sw_ns; p.sw_ks = sw_gs;
   p.a = reinterpret_cast<const uint8_t*>(qa); p.lda = lda; p.sa = sa; p.sa_rs = sa_ld; p.sa_ks = 1;
   p.out = out; p.ldo = ldo; p.out_f16 = out_dtype == STRIX_F16;
   p.M = (int)M; p.N = (int)N; p.K = (int)K; p.n_out = (int)N;
-  return dense_dispatch<kI8Group, kEpiStore>(p, as_stream(stream), op, cfg);
+  if (w_excess128) return dense_dispatch<kI8Group, kEpiStore, true>(p, as_stream(stream), op, cfg);
+  return dense_dispatch<kI8Group, kEpiStore, false>(p, as_stream(stream), op, cfg);
 }
 
 int strix_moe_gemm_fp8_w8a8(void* c, int64_t ldc, int c_dtype, const uint8_t* qa, int64_t lda,

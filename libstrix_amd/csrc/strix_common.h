@@ -136,6 +136,17 @@ __device__ __forceinline__ void g2l_b32(const void* gptr, void* lds_base) {
 // Wait until every global->LDS copy this wave issued has landed.
 __device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// Workgroup barrier for LDS hand-offs that leaves global->LDS copies in
+// flight. __syncthreads() carries a release fence, for which the compiler
+// waits on every outstanding vector memory operation (vmcnt(0)), draining a
+// multi-stage copy pipeline at each barrier. Here the caller waits for the
+// copies it needs with an explicit vmcnt; the barrier only orders this wave's
+// LDS reads (lgkmcnt(0)) and, through the memory clobber, keeps the compiler
+// from moving LDS accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // ------------------------------------------------------------------ activations
 enum Act : int { kActSilu = 0, kActGeluTanh = 1 };
 
