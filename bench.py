@@ -1,0 +1,302 @@
+#!/usr/bin/env python3
+# SPDX-License-Identifier: MIT
+"""Benchmark of the MI355X quantized-GEMM hot path.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-points] [--no-cpu]
+
+Headline (BASELINE.json metric, config 2 at M=4096): one step is the FP8-block
+W8A8 linear x[4096, 5120] bf16 -> e4m3 1x128 quant -> e4m3 MFMA GEMM against
+W[17408, 5120] e4m3 with 128x128 scales -> bf16 [4096, 17408], inputs resident
+in HBM. `value` is TFLOP/s over the whole step (2*M*N*K per step); `roofline`
+is the GEMM kernel alone against MI355X's dense-FP8 peak, timed with HIP
+events on the stream it is launched on. `points` carries every configured
+shape of BASELINE.json (decode points with cold weights: several weight sets
+rotated past the 256 MB Infinity Cache). `cpu_baseline` times the oracle's
+dequantize-then-fp32-matmul restatement on the host cores on a bounded sample.
+
+Prints ONE JSON line. One GPU only: the path runs on one MI355X.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_FP8_TFLOPS = 5000.0   # MI355X dense FP8 (no sparsity)
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense BF16
+PEAK_INT8_TOPS = 5000.0
+PEAK_HBM_GBS = 8000.0
+MALL_BYTES = 256 << 20
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+class Timer:
+    """HIP-event timing of `fn` on the current stream (the one the ops launch on)."""
+
+    def __init__(self, torch):
+        self.torch = torch
+
+    def __call__(self, fn, iters: int, warmup: int = 2) -> float:
+        torch = self.torch
+        for _ in range(warmup):
+            fn(0)
+        torch.cuda.synchronize()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        for i in range(iters):
+            fn(i)
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) * 1e3 / iters  # us
+
+
+def fp8_bytes(m, n, k):
+    return n * k + ((n + 127) // 128) * (k // 128) * 4 + m * k * 2 + m * n * 2
+
+
+def headline(torch, S, timer, steps, warmup):
+    from libstrix_amd import workloads
+
+    m, n, k = 4096, 17408, 5120
+    d = workloads.c2_fp8(seed=2, m=m, n=n, k=k, device="cuda")
+    x, w, sw = d["x"], d["w"], d["sw"]
+
+    def step(_):
+        q, s = S.fp8_quant_group128(x)
+        return S.fp8_w8a8_block_gemm(q, s, w, sw)
+
+    for _ in range(warmup):
+        step(0)
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for i in range(steps):
+        step(i)
+    t1.record()
+    torch.cuda.synchronize()
+    ms_step = t0.elapsed_time(t1) / steps
+    flops = 2.0 * m * n * k
+    value = flops / (ms_step * 1e-3) / 1e12
+    # Dominant kernel alone, same stream.
+    q, s = S.fp8_quant_group128(x)
+    us_gemm = timer(lambda _: S.fp8_w8a8_block_gemm(q, s, w, sw), iters=max(steps, 10))
+    achieved = flops / (us_gemm * 1e-6) / 1e12
+    return {
+        "ms_per_step": ms_step,
+        "value": value,
+        "gemm_us": us_gemm,
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(achieved, 1),
+            "peak": PEAK_FP8_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_FP8_TFLOPS, 4),
+            "traffic": None,
+            "kernel": "tiled8_kernel<fp8 block, 256x256>",
+            "algorithmic_flops_per_launch": flops,
+            "avg_launch_us": round(us_gemm, 2),
+        },
+        "weights": (w, sw),
+    }
+
+
+def point_c2(torch, S, timer, m, weights):
+    """FP8-block dense at M; decode M rotates cold weight sets."""
+    from libstrix_amd import workloads
+
+    n, k = 17408, 5120
+    w0, sw0 = weights
+    sets = [(w0, sw0)]
+    if m <= 256:
+        per = n * k
+        while len(sets) * per < 1.5 * MALL_BYTES:
+            sets.append((w0.clone(), sw0.clone()))
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(20 + m)).to(torch.bfloat16).cuda()
+    q, s = S.fp8_quant_group128(x)
+
+    def gemm(i):
+        w, sw = sets[i % len(sets)]
+        return S.fp8_w8a8_block_gemm(q, s, w, sw)
+
+    us_k = timer(gemm, iters=max(20, 3 * len(sets)))
+    us_op = timer(lambda i: (lambda qq: S.fp8_w8a8_block_gemm(qq[0], qq[1], *sets[i % len(sets)]))(
+        S.fp8_quant_group128(x)), iters=max(20, 3 * len(sets)))
+    flops = 2.0 * m * n * k
+    by = fp8_bytes(m, n, k)
+    res = {"M": m, "gemm_us": round(us_k, 2), "op_us": round(us_op, 2),
+           "tflops": round(flops / us_k / 1e6, 1), "gbs": round(by / us_k / 1e3, 1),
+           "frac_fp8_mfma": round(flops / us_k / 1e6 / PEAK_FP8_TFLOPS, 4),
+           "frac_hbm": round(by / us_k / 1e3 / PEAK_HBM_GBS, 4), "cold_weight_sets": len(sets)}
+    del sets
+    return res
+
+
+def point_c1(torch, S, timer):
+    from libstrix_amd import workloads
+
+    d = workloads.c1_int8(seed=1, device="cuda")
+    m, k = d["x"].shape
+    n = d["w"].shape[0]
+    sets = [(d["w"], d["sw"])]
+    while len(sets) * n * k < 1.5 * MALL_BYTES:
+        sets.append((d["w"].clone(), d["sw"].clone()))
+    x = d["x"]
+    q, s = S.int8_quant_per_token(x)
+
+    def gemm(i):
+        w, sw = sets[i % len(sets)]
+        return S.w8a8_scaled_mm(q, s, w, sw)
+
+    def op(i):
+        w, sw = sets[i % len(sets)]
+        qq, ss = S.int8_quant_per_token(x)
+        return S.w8a8_scaled_mm(qq, ss, w, sw)
+
+    us_k = timer(gemm, iters=3 * len(sets))
+    us_op = timer(op, iters=3 * len(sets))
+    by = n * k + n * 4 + m * k * 2 + m * n * 2
+    ops = 2.0 * m * n * k
+    return {"M": m, "gemm_us": round(us_k, 2), "op_us": round(us_op, 2), "gbs": round(by / us_k / 1e3, 1),
+            "frac_hbm": round(by / us_k / 1e3 / PEAK_HBM_GBS, 4), "tops": round(ops / us_k / 1e6, 2),
+            "cold_weight_sets": len(sets)}
+
+
+def moe_bytes_fp8(ids, e_h, e_i, t, h, n_experts):
+    touched = int(ids.unique().numel())
+    w = touched * (2 * e_i * e_h + e_h * e_i)
+    sc = touched * ((2 * e_i // 128) * (e_h // 128) + (e_h // 128) * (e_i // 128)) * 4
+    return w + sc + t * h * 2 * 2 + t * n_experts * 4, touched
+
+
+def point_c3(torch, S, timer, t, c3):
+    from libstrix_amd import functional
+
+    e, top_k, h, inter = 128, 8, 2048, 768
+    g = torch.Generator().manual_seed(300 + t)
+    nsets = 8 if t <= 64 else 1
+    xs = [torch.randn(t, h, generator=g).to(torch.bfloat16).cuda() for _ in range(nsets)]
+    ls = [torch.randn(t, e, generator=g).cuda() for _ in range(nsets)]
+
+    def op(i):
+        j = i % nsets
+        return functional.fused_moe_fp8_w8a8(xs[j], ls[j], c3["w13"], c3["w13_s"], c3["w2"], c3["w2_s"], top_k)
+
+    us = timer(op, iters=max(10, 2 * nsets))
+    ids, _ = S.moe_route_topk(ls[0], top_k, True)
+    by, touched = moe_bytes_fp8(ids, h, inter, t, h, e)
+    flops = 2.0 * t * top_k * (2 * inter * h + h * inter)
+    return {"T": t, "op_us": round(us, 2), "tflops": round(flops / us / 1e6, 2), "gbs": round(by / us / 1e3, 1),
+            "frac_fp8_mfma": round(flops / us / 1e6 / PEAK_FP8_TFLOPS, 4),
+            "frac_hbm": round(by / us / 1e3 / PEAK_HBM_GBS, 4), "experts_touched": touched}
+
+
+def cpu_baseline(torch):
+    """The oracle's dequantize-then-fp32-matmul on the host, config 2 weights,
+    a sample of 128 activation rows (full weight dequant each call, as the
+    reference's torch path does)."""
+    import oracle
+    from libstrix_amd import workloads
+
+    threads = min(len(os.sched_getaffinity(0)), int(os.environ.get("OMP_NUM_THREADS", "64")))
+    torch.set_num_threads(threads)
+    m, n, k = 128, 17408, 5120
+    d = workloads.c2_fp8(seed=2, m=m, n=n, k=k)
+    times = []
+    for it in range(3):
+        t0 = time.perf_counter()
+        qa, sa = oracle.fp8_quant_group128(d["x"])
+        oracle.fp8_block_gemm(qa, sa, d["w"], d["sw"])
+        times.append(time.perf_counter() - t0)
+    t = sorted(times)[1]
+    flops = 2.0 * m * n * k
+    return {"value": round(flops / t / 1e9, 2), "unit": "GFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"config 2 FP8-block W8A8, M={m} rows of 4096, N={n}, K={k}; act QDQ + full weight "
+                      f"dequant + fp32 matmul per call, median of 3 ({t * 1e3:.0f} ms)",
+            "seconds_per_call": round(t, 3)}
+
+
+def traffic_from_profile():
+    path = os.path.join(ROOT, "profiles", "fp8_w8a8_block_gemm_m4096_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return None
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-points", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}): the quantized-GEMM path "
+              "is a single-GPU kernel library; multi-GPU sharding is design-only.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import libstrix_amd
+    from libstrix_amd import workloads
+
+    if not libstrix_amd.library_available():
+        raise SystemExit("libstrix_amd/_strix_amd.so is not built (python -m libstrix_amd.build)")
+    S = torch.ops.strix
+    timer = Timer(torch)
+    log("bench: headline config 2, M=4096")
+    h = headline(torch, S, timer, args.steps, args.warmup)
+    roof = h["roofline"]
+    traffic = traffic_from_profile()
+    if traffic:
+        roof["traffic"] = traffic.get("bytes_per_launch")
+    out = {
+        "metric": "quant GEMM TFLOP/s %MFMA peak (M≥256); HBM GB/s %peak (M≤16)",
+        "value": round(h["value"], 1),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(h["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8_e4m3 (fp32 accumulate, bf16 out)",
+        "data": "synthetic (seeded CPU generator, BASELINE.json config shapes)",
+        "config": {"workload": "config 2: FP8-block W8A8 dense linear, M=4096 N=17408 K=5120, "
+                               "e4m3 1x128 activation quant + e4m3 MFMA GEMM, 128x128 weight scales"},
+        "roofline": roof,
+    }
+    points = {}
+    if not args.no_points:
+        log("bench: config 2 sweep")
+        points["c2_fp8_dense"] = [point_c2(torch, S, timer, m, h["weights"]) for m in (1, 16, 256, 4096)]
+        log("bench: config 1")
+        points["c1_int8_dense_m32"] = point_c1(torch, S, timer)
+        log("bench: config 3")
+        c3 = workloads.c3_fp8_moe(seed=3, t=1, device="cuda")
+        points["c3_fp8_moe"] = [point_c3(torch, S, timer, t, c3) for t in (1, 64, 4096)]
+        del c3
+        out["points"] = points
+    del h
+    if not args.no_cpu:
+        log("bench: cpu baseline")
+        out["cpu_baseline"] = cpu_baseline(torch)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()
