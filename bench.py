@@ -201,6 +201,22 @@ def point_c3(torch, S, timer, t, c3):
             "frac_hbm": round(by / us / 1e3 / PEAK_HBM_GBS, 4), "experts_touched": touched}
 
 
+def point_moe16(torch, S, timer, name, t, d, run, bytes_per_expert, e, top_k, h, inter):
+    """A bf16-MFMA fused MoE point (configs 4, 5): weights of the touched experts + activations."""
+    g = torch.Generator().manual_seed(700 + t)
+    nsets = 8 if t <= 64 else 1
+    xs = [torch.randn(t, h, generator=g).to(torch.bfloat16).cuda() for _ in range(nsets)]
+    ls = [torch.randn(t, e, generator=g).cuda() for _ in range(nsets)]
+    us = timer(lambda i: run(xs[i % nsets], ls[i % nsets]), iters=max(10, 2 * nsets))
+    ids, _ = S.moe_route_topk(ls[0], top_k, True)
+    touched = int(ids.unique().numel())
+    by = touched * bytes_per_expert + t * h * 2 * 2 + t * e * 4
+    flops = 2.0 * t * top_k * (2 * inter * h + h * inter)
+    return {"T": t, "op_us": round(us, 2), "tflops": round(flops / us / 1e6, 2), "gbs": round(by / us / 1e3, 1),
+            "frac_bf16_mfma": round(flops / us / 1e6 / PEAK_BF16_TFLOPS, 4),
+            "frac_hbm": round(by / us / 1e3 / PEAK_HBM_GBS, 4), "experts_touched": touched, "config": name}
+
+
 def cpu_baseline(torch):
     """The oracle's dequantize-then-fp32-matmul on the host, config 2 weights,
     a sample of 128 activation rows (full weight dequant each call, as the
@@ -290,6 +306,23 @@ def main() -> None:
         c3 = workloads.c3_fp8_moe(seed=3, t=1, device="cuda")
         points["c3_fp8_moe"] = [point_c3(torch, S, timer, t, c3) for t in (1, 64, 4096)]
         del c3
+        from libstrix_amd import functional
+
+        log("bench: config 4")
+        c4 = workloads.c4_mxfp4_moe(seed=4, t=1, device="cuda")
+        per4 = 2 * 2880 * 2880 // 2 + 2 * 2880 * 90 + 2880 * 2880 // 2 + 2880 * 90
+        run4 = lambda x, lg: functional.fused_moe_mxfp4(x, lg, c4["w13"], c4["w13_s"], c4["w2"], c4["w2_s"], 4)
+        points["c4_mxfp4_moe"] = [point_moe16(torch, S, timer, "c4", t, c4, run4, per4, 32, 4, 2880, 2880)
+                                  for t in (1, 2048)]
+        del c4
+        log("bench: config 5")
+        c5 = workloads.c5_wna16_moe(seed=5, t=1, device="cuda")
+        per5 = (1536 * 2048 + 2048 * 768) // 2 + (1536 * 16 + 2048 * 6) * 2 + (768 * 16 + 1024 * 6)
+        run5 = lambda x, lg: functional.fused_moe_wna16(x, lg, c5["w13"], c5["w13_s"], c5["w13_z"], c5["w2"],
+                                                        c5["w2_s"], c5["w2_z"], 8, 128)
+        points["c5_wna16_moe"] = [point_moe16(torch, S, timer, "c5", t, c5, run5, per5, 128, 8, 2048, 768)
+                                  for t in (1, 8192)]
+        del c5
         out["points"] = points
     del h
     if not args.no_cpu:

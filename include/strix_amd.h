@@ -101,6 +101,54 @@ int strix_moe_gemm_fp8_w8a8(void* c, int64_t ldc, int c_dtype, const uint8_t* qa
                             int64_t top_k, int64_t block_m, int silu_mul, int activation, int64_t N,
                             int64_t K, void* stream);
 
+/* ------------------------------------------------------------------ 16-bit MFMA GEMMs over dequantized weights
+ * Common MoE arguments (STRIX_MOE16_ARGS in gemm16.hip): c [num_slots, ldc]
+ * (N/2 columns when silu_mul), activations a [rows, lda] (bf16 or fp16; a
+ * row is slot / top_k), routing tensors as for strix_moe_gemm_fp8_w8a8,
+ * N = weight rows per expert, K. Scale dtype codes: 0 f32, 1 bf16, 2 f16, 3 e8m0.
+ * Weight strides (w_es, ldw) are in bytes. */
+#define STRIX_MOE16_PARAMS                                                                                         \
+  void *c, int64_t ldc, int c_dtype, const void *a, int64_t lda, int a_dtype, const int32_t *sorted_ids,          \
+      int64_t sorted_len, const int32_t *expert_ids, int64_t num_blocks, const int32_t *num_post,                 \
+      const float *topk_weights, int64_t num_slots, int64_t top_k, int64_t block_m, int silu_mul, int activation, \
+      int64_t N, int64_t K, void *stream
+/* MXFP4 experts: e2m1 [E, N, K/2] + e8m0 [E, N, K/32]; decoded to bf16 in LDS,
+ * bf16 MFMA. Absent in the reference (its MXFP4 path is dense only,
+ * csrc/gemm/mxfp4_wmma_gemm.hip:45-390); config 4. */
+int strix_moe_gemm_mxfp4(const uint8_t* w, int64_t w_es, int64_t ldw, const uint8_t* scales, int64_t s_es,
+                         int64_t s_ns, STRIX_MOE16_PARAMS);
+/* WNA16 int4 experts with zero points: uint4 [E, N, K/2] (= int32 [E, N, K/8]),
+ * scales [E, N, K/G], zeros uint8 [E, N/2, K/G]; value (q - z) s. The reference
+ * rejects zero points (python/strix_vllm/moe.py:376); config 5. */
+int strix_moe_gemm_w4a16_zp(const uint8_t* w, int64_t w_es, int64_t ldw, const void* scales, int s_kind,
+                            int64_t s_es, int64_t s_ns, const uint8_t* zeros, int64_t z_es, int64_t z_ns,
+                            int64_t group, STRIX_MOE16_PARAMS);
+/* moe_gemm_w4a16 (csrc/torch_ops.cpp:191-195): symmetric (q - 8) s. */
+int strix_moe_gemm_w4a16(const uint8_t* w, int64_t w_es, int64_t ldw, const void* scales, int s_kind, int64_t s_es,
+                         int64_t s_ns, int64_t group, STRIX_MOE16_PARAMS);
+/* moe_gemm_bf16 (csrc/torch_ops.cpp:185-189): bf16 experts; w_es and ldw in elements here. */
+int strix_moe_gemm_bf16(const uint16_t* w, int64_t w_es, int64_t ldw, STRIX_MOE16_PARAMS);
+/* moe_gemm_fp8 / moe_gemm_fp8_raw (csrc/torch_ops.cpp:225-232): e4m3 experts,
+ * W8A16 (bf16 or fp16 activations), block [E, N/128, K/128] or channel [E, N] scales. */
+int strix_moe_gemm_fp8_w8a16(const uint8_t* w, int64_t w_es, int64_t ldw, const void* scales, int s_kind,
+                             int64_t s_es, int64_t s_ns, int64_t s_ks, int block_scales, STRIX_MOE16_PARAMS);
+/* moe_gemm_w8a16 (csrc/torch_ops.cpp:221-224): int8 experts, per-channel scales. */
+int strix_moe_gemm_w8a16(const int8_t* w, int64_t w_es, int64_t ldw, const void* scales, int s_kind, int64_t s_es,
+                         int64_t s_ns, STRIX_MOE16_PARAMS);
+/* mxfp4_wmma_gemm (csrc/torch_ops.cpp:283-286): dense MXFP4 W4A16 (+ bias, bias_rs 0 = [N]). */
+int strix_mxfp4_gemm(const uint8_t* w, int64_t ldw, const uint8_t* scales, int64_t s_ld, const void* x, int x_dtype,
+                     int64_t ldx, const void* bias, int64_t bias_rs, void* out, int64_t ldo, int out_dtype, int64_t M,
+                     int64_t N, int64_t K, int cfg, void* stream);
+/* fp8_wmma_gemm(_raw) (csrc/torch_ops.cpp:253-256): dense FP8 W8A16. */
+int strix_fp8_w8a16_gemm(const uint8_t* w, int64_t ldw, const float* scales, int64_t s_ld, int block_scales,
+                         const void* x, int x_dtype, int64_t ldx, void* out, int64_t ldo, int out_dtype, int64_t M,
+                         int64_t N, int64_t K, int cfg, void* stream);
+/* Whole-matrix dequant to bf16 (mxfp4_dequant, fp8_dequant, csrc/torch_ops.cpp:252, 294):
+ * fmt 1 MXFP4, 4 FP8 (kgroup 128 + nblock 128 for block scales, kgroup 0 for channel),
+ * 3 INT4 symmetric plain nibbles. */
+int strix_dequant_bf16(int fmt, const uint8_t* w, int64_t ldw, const void* scales, int s_kind, int64_t s_ld,
+                       int64_t kgroup, int64_t nblock, uint16_t* out, int64_t ldo, int64_t N, int64_t K, void* stream);
+
 /* ------------------------------------------------------------------ MoE plumbing
  * Router: softmax -> top-k -> optional renormalize (vLLM fused_topk, called at
  * python/strix_vllm/moe.py:181-184). ids by logit value, ties to the lower id. */

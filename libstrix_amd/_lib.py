@@ -23,6 +23,14 @@ P = c_void_p
 I = c_int
 L = c_int64
 
+# Trailing arguments shared by the 16-bit MoE GEMMs (STRIX_MOE16_PARAMS).
+MOE16 = [P, L, I, P, L, I, P, L, P, L, P, P, L, L, L, I, I, L, L, P]
+
+# scale dtype codes of the 16-bit GEMMs
+S_F32, S_BF16, S_F16, S_E8M0 = 0, 1, 2, 3
+# weight format codes of strix_dequant_bf16
+FMT_MXFP4, FMT_INT4_SYM, FMT_FP8 = 1, 3, 4
+
 # name -> argument types (all return int unless listed in _RESTYPE)
 SIGNATURES: dict[str, list] = {
     "strix_abi_version": [],
@@ -34,6 +42,15 @@ SIGNATURES: dict[str, list] = {
     "strix_w8a8_int8_gemm": [P, L, P, P, L, P, P, L, I, L, L, L, I, P],
     "strix_w8a8_int8_group_gemm": [P, L, P, L, P, L, I, P, L, L, P, L, I, L, L, L, I, P],
     "strix_moe_gemm_fp8_w8a8": [P, L, I, P, L, P, L, P, L, L, P, L, L, P, L, P, L, P, P, L, L, L, I, I, L, L, P],
+    "strix_moe_gemm_mxfp4": [P, L, L, P, L, L] + MOE16,
+    "strix_moe_gemm_w4a16_zp": [P, L, L, P, I, L, L, P, L, L, L] + MOE16,
+    "strix_moe_gemm_w4a16": [P, L, L, P, I, L, L, L] + MOE16,
+    "strix_moe_gemm_bf16": [P, L, L] + MOE16,
+    "strix_moe_gemm_fp8_w8a16": [P, L, L, P, I, L, L, L, I] + MOE16,
+    "strix_moe_gemm_w8a16": [P, L, L, P, I, L, L] + MOE16,
+    "strix_mxfp4_gemm": [P, L, P, L, P, I, L, P, L, P, L, I, L, L, L, I, P],
+    "strix_fp8_w8a16_gemm": [P, L, P, L, I, P, I, L, P, L, I, L, L, L, I, P],
+    "strix_dequant_bf16": [I, P, L, P, I, L, L, L, P, L, L, L, P],
     "strix_moe_route_topk": [P, I, L, L, L, L, I, P, P, L, P],
     "strix_moe_align_sorted_capacity": [L, L, L],
     "strix_moe_align_workspace_bytes": [L, L],

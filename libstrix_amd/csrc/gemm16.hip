@@ -1,0 +1,774 @@
+// SPDX-License-Identifier: MIT
+// 16-bit MFMA GEMMs over dequantized weights for gfx950: bf16 (or fp16)
+// activations x weights decoded to bf16 (fp16) and contracted with
+// mfma_f32_16x16x32_bf16 (_f16). Dense and MoE (grouped over aligned sorted
+// ids), with the same fused epilogues as the 8-bit kernels.
+//
+// Weight formats (decode is exact except where a scale is applied in fp32
+// and the product rounded once to bf16/fp16):
+//   BF16      bf16 [E][N][K], copied as is
+//   MXFP4     e2m1 nibbles [E][N][K/2] (low nibble = even k) + e8m0 [E][N][K/32],
+//             value = e2m1 * 2^(e-127), e == 0 is a zero block
+//             (csrc/gemm/mxfp4_wmma_gemm.hip:14-23; tests/test_mxfp4.py:28-95)
+//   INT4_ZP   uint4 [E][N][K/2] bytes (= int32 [E][N][K/8], k = 8w+j in nibble j),
+//             scales [E][N][K/G] bf16/fp16, zero points uint8 [E][N/2][K/G]
+//             (even n in the low nibble); value = (q - z) * s
+//   INT4_SYM  same packing, value = (q - 8) * s (csrc/moe/moe_gemm_w4a16.hip:7-14)
+//   FP8       e4m3fn [E][N][K] with fp32 128x128 block scales [E][N/128][K/128]
+//             or per-channel scales [E][N] (csrc/moe/moe_gemm_w8a16.hip:15-36)
+//   INT8      int8 [E][N][K] with per-channel scales [E][N] (W8A16)
+//
+// Kernels:
+//   stream16: decode shapes. Each wave decodes its weight rows in registers
+//             (16 bytes of packed weights per lane per chunk), waves split K
+//             and reduce through LDS.
+//   tiled16:  prefill. Each 64-K stage, the block's threads decode the weight
+//             tile once into LDS (the swizzled 128-byte row layout of
+//             gemm_common.h), token rows arrive by direct global->LDS copy, and
+//             every wave reads both operands as MFMA fragments.
+#include <type_traits>
+
+#include "capi_internal.h"
+#include "gemm_common.h"
+#include "strix_common.h"
+
+namespace strix {
+namespace {
+
+enum WFmt : int { kWBf16 = 0, kWMxfp4 = 1, kWInt4Zp = 2, kWInt4Sym = 3, kWFp8 = 4, kWInt8 = 5 };
+enum SKind : int { kSF32 = 0, kSBf16 = 1, kSF16 = 2, kSE8m0 = 3 };
+
+template <int FMT>
+struct FmtInfo {
+  static constexpr int bits = (FMT == kWBf16) ? 16 : ((FMT == kWFp8 || FMT == kWInt8) ? 8 : 4);
+};
+
+struct G16 {
+  const uint8_t* w;  // weights, row stride ldw and expert stride w_es in bytes
+  int64_t ldw, w_es;
+  const void* ws;    // scales: element strides per expert / per scale row / per K group
+  int64_t ws_es, ws_ns, ws_ks;
+  int ws_kind;       // SKind
+  int ws_kgroup;     // K elements per scale along K (0: one scale for all K)
+  int ws_nblock;     // weight rows per scale row (128 for fp8 block scales, else 1)
+  const uint8_t* wz; // int4 zero points [E][N/2][K/G]
+  int64_t wz_es, wz_ns, wz_ks;
+  const uint16_t* a; // activations (bf16 or fp16), row stride lda elements
+  int64_t lda;
+  const uint16_t* bias;  // dense only: output-dtype bias, row stride bias_rs (0 = [N])
+  int64_t bias_rs;
+  void* out;
+  int64_t ldo;
+  int out_f16;
+  int M, N, K, n_out, gate_off;
+  const int32_t* sorted_ids;
+  int64_t sorted_len;
+  const int32_t* expert_ids;
+  const int32_t* num_post;
+  int num_slots, top_k;
+  const float* topk_w;
+};
+
+// Scale of weight row n (within an expert) at K position k.
+__device__ __forceinline__ float wscale(const G16& p, int e, int n, int k) {
+  const int64_t idx = (int64_t)e * p.ws_es + (int64_t)(n / p.ws_nblock) * p.ws_ns +
+                      (p.ws_kgroup ? (int64_t)(k / p.ws_kgroup) * p.ws_ks : 0);
+  switch (p.ws_kind) {
+    case kSF32: return static_cast<const float*>(p.ws)[idx];
+    case kSBf16: return bf16_bits_to_f32(static_cast<const uint16_t*>(p.ws)[idx]);
+    case kSF16: return f16_bits_to_f32(static_cast<const uint16_t*>(p.ws)[idx]);
+    default: {
+      const uint32_t b = static_cast<const uint8_t*>(p.ws)[idx];
+      return __uint_as_float(b << 23);  // 2^(b-127); b == 0 gives +0: the zero block
+    }
+  }
+}
+
+__device__ __forceinline__ float wzero(const G16& p, int e, int n, int k) {
+  const uint32_t b = p.wz[(int64_t)e * p.wz_es + (int64_t)(n >> 1) * p.wz_ns + (int64_t)(k / p.ws_kgroup) * p.wz_ks];
+  return (float)((n & 1) ? (b >> 4) : (b & 15));
+}
+
+template <bool F16>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  if constexpr (F16) return f32_to_f16_bits(lo) | (f32_to_f16_bits(hi) << 16);
+  else return pack_bf16x2(lo, hi);
+}
+
+// e2m1 magnitude code (3 bits) -> fp32 bits for a unit scale.
+__device__ __forceinline__ float e2m1_mag(uint32_t c) {
+  const uint32_t e = c >> 1, m = c & 1;
+  const uint32_t bits = e ? (((e + 126u) << 23) | (m << 22)) : (m ? 0x3f000000u : 0u);
+  return __uint_as_float(bits);
+}
+
+// Decodes one dword of packed weights (8 values for 4-bit formats, 4 for
+// 8-bit) into 16-bit values, appending to out[] as packed pairs.
+template <int FMT, bool F16>
+__device__ __forceinline__ void decode_dword(uint32_t d, float s, float z, uint32_t* out) {
+  if constexpr (FMT == kWMxfp4) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t byte = (d >> (8 * j)) & 0xffu;
+      const uint32_t lo = byte & 15u, hi = byte >> 4;
+      float vl = e2m1_mag(lo & 7u) * s, vh = e2m1_mag(hi & 7u) * s;
+      vl = (lo & 8u) ? -vl : vl;
+      vh = (hi & 8u) ? -vh : vh;
+      out[j] = pack2<F16>(vl, vh);
+    }
+  } else if constexpr (FMT == kWInt4Zp || FMT == kWInt4Sym) {
+    const uint32_t lo = d & 0x0f0f0f0fu, hi = (d >> 4) & 0x0f0f0f0fu;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float q0 = (float)((lo >> (8 * j)) & 0xffu);
+      const float q1 = (float)((hi >> (8 * j)) & 0xffu);
+      out[j] = pack2<F16>((q0 - z) * s, (q1 - z) * s);
+    }
+  } else if constexpr (FMT == kWFp8) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      out[j] = pack2<F16>(e4m3_to_f32((d >> (16 * j)) & 0xffu) * s, e4m3_to_f32((d >> (16 * j + 8)) & 0xffu) * s);
+  } else if constexpr (FMT == kWInt8) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const float v0 = (float)(int)(int8_t)((d >> (16 * j)) & 0xffu);
+      const float v1 = (float)(int)(int8_t)((d >> (16 * j + 8)) & 0xffu);
+      out[j] = pack2<F16>(v0 * s, v1 * s);
+    }
+  }
+}
+
+// ============================================================ stream16
+// Per chunk a lane holds PV consecutive K values of its weight row: 32 for
+// 4-bit weights in 16 bytes (a 64-K tail of a K that is 64 mod 128 uses 8
+// bytes, PV 16), 16 for 8-bit, 8 for bf16. MFMA step j of the chunk pairs the
+// lane's values 8j..8j+7 with the same K positions of the token rows.
+template <int FMT, int NT, int MT, int WAVES, bool MOE, int EPI, int ACT, bool F16>
+__global__ void __launch_bounds__(WAVES * 64) stream16_kernel(G16 p) {
+  constexpr int BITS = FmtInfo<FMT>::bits;
+  constexpr int PV = 128 / BITS;   // K values per lane per full chunk (16 bytes)
+  constexpr int CK = 4 * PV;       // K per full chunk
+  constexpr int NTH = (EPI == kEpiGated) ? NT / 2 : NT;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r16 = lane & 15, g4 = lane >> 4;
+  const int m0 = blockIdx.y * (16 * MT);
+  int expert = 0;
+  if constexpr (MOE) {
+    if (m0 >= *p.num_post) return;
+    expert = p.expert_ids[blockIdx.y];
+    if (expert < 0) return;
+  }
+  const int nout0 = blockIdx.x * (16 * NTH);
+  int wrow[NT];
+#pragma unroll
+  for (int s = 0; s < NT; ++s) {
+    int r;
+    if constexpr (EPI == kEpiGated) r = s < NTH ? nout0 + 16 * s : p.gate_off + nout0 + 16 * (s - NTH);
+    else r = nout0 + 16 * s;
+    wrow[s] = min(r + r16, p.N - 1);  // this lane's weight row of subtile s
+  }
+  const uint8_t* wbase = p.w + (int64_t)expert * p.w_es;
+  int brow[MT], orow[MT];
+  bool bval[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) token_row<MOE>(p, m0 + 16 * t + r16, brow[t], orow[t], bval[t]);
+
+  const int nfull = p.K / CK;
+  const bool tail = (p.K % CK) != 0;  // 4-bit only: a 64-K tail (K % 64 == 0 is required)
+  const int nch = nfull + (tail ? 1 : 0);
+  const int per = (nch + WAVES - 1) / WAVES;
+  const int c0 = min(nch, wave * per), c1 = min(nch, c0 + per);
+
+  v4f acc[NT][MT];
+#pragma unroll
+  for (int s = 0; s < NT; ++s)
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[s][t] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  auto chunk = [&](int c, auto pv_tag) {
+    constexpr int V = decltype(pv_tag)::value;  // K values per lane in this chunk
+    constexpr int STEPS = V / 8;
+    const int kc = c * CK + g4 * V;            // this lane's first K position
+    uint32_t wv[NT][V / 2];                    // decoded 16-bit pairs
+#pragma unroll
+    for (int s = 0; s < NT; ++s) {
+      const uint8_t* src = wbase + (int64_t)wrow[s] * p.ldw + (int64_t)kc * BITS / 8;
+      if constexpr (FMT == kWBf16) {
+        const u32x4 raw = ldg128(src);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) wv[s][i] = raw[i];
+      } else {
+        uint32_t raw[V * BITS / 32];
+        if constexpr (V * BITS == 128) {
+          const u32x4 r4 = ldg128(src);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) raw[i] = r4[i];
+        } else {
+          const uint2 r2 = *reinterpret_cast<const uint2*>(src);
+          raw[0] = r2.x;
+          raw[1] = r2.y;
+        }
+        const float sc = wscale(p, expert, wrow[s], kc);
+        const float z = (FMT == kWInt4Zp) ? wzero(p, expert, wrow[s], kc) : 8.0f;
+        constexpr int PAIRS_PER_DWORD = 32 / BITS / 2;
+#pragma unroll
+        for (int i = 0; i < V * BITS / 32; ++i) decode_dword<FMT, F16>(raw[i], sc, z, &wv[s][i * PAIRS_PER_DWORD]);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      const uint16_t* ar = p.a + (int64_t)brow[t] * p.lda + kc;
+#pragma unroll
+      for (int j = 0; j < STEPS; ++j) {
+        const u32x4 av = ldg128(ar + 8 * j);
+#pragma unroll
+        for (int s = 0; s < NT; ++s) {
+          u32x4 wq;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) wq[i] = wv[s][4 * j + i];
+          if constexpr (F16)
+            acc[s][t] = mfma_f16(__builtin_bit_cast(f16x8, wq), __builtin_bit_cast(f16x8, av), acc[s][t]);
+          else
+            acc[s][t] = mfma_bf16(__builtin_bit_cast(bf16x8, wq), __builtin_bit_cast(bf16x8, av), acc[s][t]);
+        }
+      }
+    }
+  };
+  for (int c = c0; c < c1; ++c) {
+    if (FMT != kWBf16 && BITS == 4 && tail && c == nfull) chunk(c, std::integral_constant<int, PV / 2>{});
+    else chunk(c, std::integral_constant<int, PV>{});
+  }
+
+  constexpr int TILES = NT * MT;
+  __shared__ float red[WAVES > 1 ? WAVES * TILES * 4 * 64 : 1];
+  if constexpr (WAVES > 1) {
+#pragma unroll
+    for (int s = 0; s < NT; ++s)
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) red[((wave * TILES + s * MT + t) * 4 + i) * 64 + lane] = acc[s][t][i];
+    __syncthreads();
+  }
+#pragma unroll
+  for (int so = 0; so < NTH; ++so)
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      const int o = so * MT + t;
+      if (WAVES > 1 && (o % WAVES) != wave) continue;
+      float g[4], u[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if constexpr (WAVES > 1) {
+          float sg = 0.f, su = 0.f;
+          for (int w = 0; w < WAVES; ++w) {
+            sg += red[((w * TILES + so * MT + t) * 4 + i) * 64 + lane];
+            if constexpr (EPI == kEpiGated) su += red[((w * TILES + (so + NTH) * MT + t) * 4 + i) * 64 + lane];
+          }
+          g[i] = sg;
+          u[i] = su;
+        } else {
+          g[i] = acc[so][t][i];
+          u[i] = (EPI == kEpiGated) ? acc[so + NTH][t][i] : 0.f;
+        }
+      }
+      if (!bval[t]) continue;
+      const int col0 = nout0 + 16 * so + 4 * g4;
+      if constexpr (!MOE && EPI == kEpiStore) {
+        if (p.bias) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (col0 + i < p.n_out) {
+              const uint32_t b = p.bias[(int64_t)orow[t] * p.bias_rs + col0 + i];
+              g[i] += p.out_f16 ? f16_bits_to_f32(b) : bf16_bits_to_f32(b);
+            }
+        }
+      }
+      finish_float4<EPI, ACT, MOE>(p, orow[t], col0, g, u);
+    }
+}
+
+// ============================================================ tiled16
+// One 64-K stage per LDS buffer: weight rows 0..BN-1 (decoded by the block's
+// threads), token rows BN..BN+BM-1 (direct copies), 128 bytes per row,
+// swizzled. Three buffers: while stage kb is computed, stage kb+1 is decoded
+// and stage kb+2 is in flight.
+template <int FMT, int BM, int BN, int WM, int WN, bool MOE, int EPI, int ACT, bool F16>
+__global__ void __launch_bounds__(WM * WN * 64) tiled16_kernel(G16 p, int tiles_m, int tiles_n, int group_m) {
+  constexpr int W = WM * WN, T = W * 64;
+  constexpr int TM = BM / WM, TN = BN / WN;
+  constexpr int MT = TM / 16, NT = TN / 16;
+  constexpr int SA = BN / 16;
+  constexpr int STAGES = 3;
+  constexpr int STAGE = (BN + BM) * 128;
+  constexpr int BITS = FmtInfo<FMT>::bits;
+  constexpr bool DIRECT_W = (FMT == kWBf16);
+  constexpr int PV = DIRECT_W ? 8 : 128 / BITS;  // K values per 16-byte weight piece
+  constexpr int PPR = 64 / PV;                   // pieces per row per stage
+  constexpr int PIECES = BN * PPR;
+  constexpr int PPT = DIRECT_W ? 0 : (PIECES + T - 1) / T;  // pieces per thread (the last round may be partial)
+  constexpr int ACOPY = BM / 8;                  // token row copies (8 rows each)
+  constexpr int WCOPY = DIRECT_W ? BN / 8 : 0;
+  static_assert((ACOPY + WCOPY) % W == 0, "copies split evenly over the waves");
+  constexpr int CPW = (ACOPY + WCOPY) / W;
+  constexpr bool GATED = (EPI == kEpiGated);
+  constexpr int NTH = GATED ? NT / 2 : NT;
+  static_assert(!GATED || NT % 2 == 0, "gated wave tiles pair gate and up subtiles");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * STAGE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, g4 = lane >> 4;
+  const int wm = wave % WM, wn = wave / WM;
+  int tm, tn, expert = 0;
+  if constexpr (MOE) {
+    tn = blockIdx.x;
+    tm = blockIdx.y;
+    if (tm * BM >= *p.num_post) return;
+    expert = p.expert_ids[tm];
+    if (expert < 0) return;
+  } else {
+    dense_tile(blockIdx.x, tiles_m, tiles_n, group_m, tm, tn);
+  }
+  const int m0 = tm * BM;
+  auto wrow_of = [&](int r) -> int {  // weight row of LDS weight row r (0..BN-1)
+    if constexpr (GATED) {
+      const int base = tn * (BN / 2);
+      return r < BN / 2 ? base + r : p.gate_off + base + (r - BN / 2);
+    } else {
+      return tn * BN + r;
+    }
+  };
+  const uint8_t* wbase = p.w + (int64_t)expert * p.w_es;
+
+  // Direct copies (token rows, and bf16 weight rows): 8 rows x 128 B each.
+  uint32_t qoff[CPW > 0 ? CPW : 1];
+  bool qis_w[CPW > 0 ? CPW : 1];
+#pragma unroll
+  for (int j = 0; j < CPW; ++j) {
+    const int q = wave + W * j;
+    const int row = 8 * q + (lane >> 3);  // LDS row: weights first when copied directly
+    if (DIRECT_W && row < BN) {
+      const int r = min(wrow_of(row), p.N - 1);
+      qoff[j] = (uint32_t)r * (uint32_t)p.ldw;
+      qis_w[j] = true;
+    } else {
+      const int trow = DIRECT_W ? row - BN : row;
+      int br, orw;
+      bool v;
+      token_row<MOE>(p, m0 + trow, br, orw, v);
+      qoff[j] = (uint32_t)br * (uint32_t)(p.lda * 2);
+      qis_w[j] = false;
+    }
+    qoff[j] += 16 * ((lane & 7) ^ lds_swz(row + (DIRECT_W ? 0 : BN)));
+  }
+  // Decoded weight pieces of this thread: (LDS row, piece index within the row).
+  int prow[PPT > 0 ? PPT : 1], pidx[PPT > 0 ? PPT : 1], pgrow[PPT > 0 ? PPT : 1];
+#pragma unroll
+  for (int j = 0; j < PPT; ++j) {
+    const int pi = min(tid + T * j, PIECES - 1);  // surplus threads repeat the last piece (same bytes, same slot)
+    prow[j] = pi / PPR;
+    pidx[j] = pi % PPR;
+    pgrow[j] = min(wrow_of(prow[j]), p.N - 1);
+  }
+  u32x4 wraw[PPT > 0 ? PPT : 1];
+
+  auto load_w = [&](int kb) {
+#pragma unroll
+    for (int j = 0; j < PPT; ++j)
+      wraw[j] = ldg128(wbase + (int64_t)pgrow[j] * p.ldw + (int64_t)(kb * 64 + pidx[j] * PV) * BITS / 8);
+  };
+  auto copy_a = [&](int kb, int buf) {
+    uint8_t* st = smem + buf * STAGE;
+#pragma unroll
+    for (int j = 0; j < CPW; ++j) {
+      const int q = wave + W * j;
+      const uint8_t* base = qis_w[j] ? wbase + (int64_t)kb * 128 : reinterpret_cast<const uint8_t*>(p.a) + (int64_t)kb * 128;
+      g2l_b128(base + qoff[j], st + (DIRECT_W ? q : q + BN / 8) * 1024);
+    }
+  };
+  auto decode_w = [&](int kb, int buf) {
+    uint8_t* st = smem + buf * STAGE;
+#pragma unroll
+    for (int j = 0; j < PPT; ++j) {
+      const int k = kb * 64 + pidx[j] * PV;
+      const float sc = wscale(p, expert, pgrow[j], k);
+      const float z = (FMT == kWInt4Zp) ? wzero(p, expert, pgrow[j], k) : 8.0f;
+      uint32_t v[PV / 2];
+      constexpr int PAIRS_PER_DWORD = 32 / BITS / 2;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) decode_dword<FMT, F16>(wraw[j][i], sc, z, &v[i * PAIRS_PER_DWORD]);
+      const int row = prow[j];
+#pragma unroll
+      for (int c = 0; c < PV / 8; ++c) {
+        const int chunk = pidx[j] * (PV / 8) + c;
+        u32x4 o;
+        o[0] = v[4 * c]; o[1] = v[4 * c + 1]; o[2] = v[4 * c + 2]; o[3] = v[4 * c + 3];
+        *reinterpret_cast<u32x4*>(st + row * 128 + 16 * (chunk ^ lds_swz(row))) = o;
+      }
+    }
+  };
+
+  int aidx[NT];
+#pragma unroll
+  for (int s = 0; s < NT; ++s) {
+    if constexpr (GATED) aidx[s] = s < NTH ? wn * NTH + s : SA / 2 + wn * NTH + (s - NTH);
+    else aidx[s] = wn * NT + s;
+  }
+  const uint32_t frag0 = (uint32_t)r16 * 128 + 16 * ((g4) ^ lds_swz(r16));
+  const uint32_t frag1 = (uint32_t)r16 * 128 + 16 * ((4 + g4) ^ lds_swz(r16));
+
+  v4f acc[NT][MT];
+#pragma unroll
+  for (int s = 0; s < NT; ++s)
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[s][t] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  const int nkb = p.K >> 6;
+  load_w(0);
+  copy_a(0, 0);
+  wait_vmcnt<0>();
+  decode_w(0, 0);
+  if (nkb > 1) {
+    load_w(1);
+    copy_a(1, 1);
+  }
+  for (int kb = 0; kb < nkb; ++kb) {
+    wait_vmcnt<0>();
+    if (kb + 1 < nkb) decode_w(kb + 1, (kb + 1) % STAGES);
+    lds_barrier();
+    if (kb + 2 < nkb) {
+      load_w(kb + 2);
+      copy_a(kb + 2, (kb + 2) % STAGES);
+    }
+    const uint8_t* st = smem + (kb % STAGES) * STAGE;
+#pragma unroll
+    for (int step = 0; step < 2; ++step) {
+      const uint32_t fo = step ? frag1 : frag0;
+      u32x4 bf[MT];
+#pragma unroll
+      for (int t = 0; t < MT; ++t) bf[t] = lds128(st + (SA + wm * MT + t) * 2048 + fo);
+#pragma unroll
+      for (int s = 0; s < NT; ++s) {
+        const u32x4 af = lds128(st + aidx[s] * 2048 + fo);
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          if constexpr (F16)
+            acc[s][t] = mfma_f16(__builtin_bit_cast(f16x8, af), __builtin_bit_cast(f16x8, bf[t]), acc[s][t]);
+          else
+            acc[s][t] = mfma_bf16(__builtin_bit_cast(bf16x8, af), __builtin_bit_cast(bf16x8, bf[t]), acc[s][t]);
+        }
+      }
+    }
+  }
+
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    int br, orw;
+    bool v;
+    token_row<MOE>(p, m0 + wm * TM + 16 * t + r16, br, orw, v);
+    if (!v) continue;
+#pragma unroll
+    for (int so = 0; so < NTH; ++so) {
+      float g[4], u[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        g[i] = acc[so][t][i];
+        u[i] = GATED ? acc[so + NTH][t][i] : 0.f;
+      }
+      const int col0 = GATED ? (tn * (BN / 2) + 16 * (wn * NTH + so) + 4 * g4) : (tn * BN + 16 * (wn * NT + so) + 4 * g4);
+      if constexpr (!MOE && EPI == kEpiStore) {
+        if (p.bias) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (col0 + i < p.n_out) {
+              const uint32_t b = p.bias[(int64_t)orw * p.bias_rs + col0 + i];
+              g[i] += p.out_f16 ? f16_bits_to_f32(b) : bf16_bits_to_f32(b);
+            }
+        }
+      }
+      finish_float4<EPI, ACT, MOE>(p, orw, col0, g, u);
+    }
+  }
+}
+
+// ============================================================ whole-matrix dequant
+// out[n, k] = decode(w[n, k]) in bf16; one thread per 16-byte piece.
+template <int FMT>
+__global__ void __launch_bounds__(256) dequant_kernel(G16 p, uint16_t* out, int64_t ldo) {
+  constexpr int BITS = FmtInfo<FMT>::bits;
+  constexpr int PV = 128 / BITS;
+  const int64_t pieces_per_row = p.K / PV;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)p.N * pieces_per_row) return;
+  const int n = (int)(i / pieces_per_row);
+  const int k = (int)(i % pieces_per_row) * PV;
+  const u32x4 raw = ldg128(p.w + (int64_t)n * p.ldw + (int64_t)k * BITS / 8);
+  const float sc = wscale(p, 0, n, k);
+  const float z = (FMT == kWInt4Zp) ? wzero(p, 0, n, k) : 8.0f;
+  uint32_t v[PV / 2];
+  constexpr int PAIRS_PER_DWORD = 32 / BITS / 2;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) decode_dword<FMT, false>(raw[j], sc, z, &v[j * PAIRS_PER_DWORD]);
+  uint16_t* o = out + (int64_t)n * ldo + k;
+#pragma unroll
+  for (int c = 0; c < PV / 8; ++c) {
+    u32x4 q;
+    q[0] = v[4 * c]; q[1] = v[4 * c + 1]; q[2] = v[4 * c + 2]; q[3] = v[4 * c + 3];
+    *reinterpret_cast<u32x4*>(o + 8 * c) = q;
+  }
+}
+
+// ============================================================ launchers
+template <int FMT, int NT, int MT, int WAVES, bool MOE, int EPI, int ACT, bool F16>
+int launch_stream16(const G16& p, int grid_y, hipStream_t st, const char* op) {
+  constexpr int NTH = (EPI == kEpiGated) ? NT / 2 : NT;
+  const int grid_x = (p.n_out + 16 * NTH - 1) / (16 * NTH);
+  hipLaunchKernelGGL((stream16_kernel<FMT, NT, MT, WAVES, MOE, EPI, ACT, F16>), dim3(grid_x, grid_y), dim3(WAVES * 64), 0,
+                     st, p);
+  return check_launch(op);
+}
+
+template <int FMT, int BM, int BN, int WM, int WN, bool MOE, int EPI, int ACT, bool F16>
+int launch_tiled16(const G16& p, int grid_y_moe, hipStream_t st, const char* op) {
+  constexpr int COLS = (EPI == kEpiGated) ? BN / 2 : BN;
+  const int tiles_n = (p.n_out + COLS - 1) / COLS;
+  if constexpr (MOE) {
+    hipLaunchKernelGGL((tiled16_kernel<FMT, BM, BN, WM, WN, MOE, EPI, ACT, F16>), dim3(tiles_n, grid_y_moe),
+                       dim3(WM * WN * 64), 0, st, p, 0, tiles_n, 0);
+  } else {
+    const int tiles_m = (p.M + BM - 1) / BM;
+    hipLaunchKernelGGL((tiled16_kernel<FMT, BM, BN, WM, WN, MOE, EPI, ACT, F16>), dim3(tiles_m * tiles_n),
+                       dim3(WM * WN * 64), 0, st, p, tiles_m, tiles_n, 8);
+  }
+  return check_launch(op);
+}
+
+template <int FMT, int EPI, int ACT, bool F16>
+int moe16_dispatch(const G16& p, int block_m, int num_blocks, hipStream_t st, const char* op) {
+  constexpr int NTS = (EPI == kEpiGated) ? 2 : 1;
+  switch (block_m) {
+    case 16: return launch_stream16<FMT, NTS, 1, 4, true, EPI, ACT, F16>(p, num_blocks, st, op);
+    case 32: return launch_stream16<FMT, NTS, 2, 4, true, EPI, ACT, F16>(p, num_blocks, st, op);
+    case 64: return launch_tiled16<FMT, 64, 128, 1, 4, true, EPI, ACT, F16>(p, num_blocks, st, op);
+    case 128: return launch_tiled16<FMT, 128, 128, 2, 2, true, EPI, ACT, F16>(p, num_blocks, st, op);
+    case 256: return launch_tiled16<FMT, 256, 128, 4, 2, true, EPI, ACT, F16>(p, num_blocks, st, op);
+    default: return set_error(STRIX_ERR_INVALID, "%s: block_m must be 16, 32, 64, 128 or 256, got %d", op, block_m);
+  }
+}
+
+template <int FMT, bool F16>
+int dense16_dispatch(const G16& p, hipStream_t st, const char* op, int cfg) {
+  const int M = p.M;
+  if (cfg < 0) cfg = M <= 16 ? 0 : (M <= 32 ? 1 : (M <= 64 ? 2 : 3));
+  switch (cfg) {
+    case 0: return launch_stream16<FMT, 1, 1, 8, false, kEpiStore, kActSilu, F16>(p, (M + 15) / 16, st, op);
+    case 1: return launch_stream16<FMT, 1, 2, 8, false, kEpiStore, kActSilu, F16>(p, (M + 31) / 32, st, op);
+    case 2: return launch_stream16<FMT, 1, 4, 4, false, kEpiStore, kActSilu, F16>(p, (M + 63) / 64, st, op);
+    case 3: return launch_tiled16<FMT, 128, 128, 2, 2, false, kEpiStore, kActSilu, F16>(p, 0, st, op);
+    case 4: return launch_tiled16<FMT, 256, 128, 4, 2, false, kEpiStore, kActSilu, F16>(p, 0, st, op);
+    case 5: return launch_tiled16<FMT, 64, 128, 1, 4, false, kEpiStore, kActSilu, F16>(p, 0, st, op);
+    default: return set_error(STRIX_ERR_INVALID, "%s: cfg must be in 0..5, got %d", op, cfg);
+  }
+}
+
+// ------------------------------------------------------------ argument checks
+int check_scale_kind(const char* op, int kind) {
+  STRIX_REQUIRE(kind >= kSF32 && kind <= kSE8m0, "%s: unknown scale dtype code %d", op, kind);
+  return STRIX_OK;
+}
+
+struct MoeArgs {
+  void* c; int64_t ldc; int c_dtype;
+  const void* a; int64_t lda; int a_dtype;
+  const int32_t* sorted_ids; int64_t sorted_len; const int32_t* expert_ids; int64_t num_blocks;
+  const int32_t* num_post; const float* topk_w; int64_t num_slots; int64_t top_k; int64_t block_m;
+  int silu_mul; int activation; int64_t N; int64_t K;
+};
+
+template <int FMT>
+int run_moe16(const char* op, const MoeArgs& m, G16 p, void* stream) {
+  STRIX_REQUIRE(m.a_dtype == STRIX_BF16 || m.a_dtype == STRIX_F16, "%s: activations must be bfloat16 or float16", op);
+  STRIX_REQUIRE(m.c_dtype == STRIX_BF16 || m.c_dtype == STRIX_F16, "%s: output must be bfloat16 or float16", op);
+  STRIX_REQUIRE(m.K % 64 == 0, "%s: K must be a multiple of 64, got K=%lld", op, (long long)m.K);
+  STRIX_REQUIRE(m.N % 16 == 0 && (!m.silu_mul || m.N % 32 == 0), "%s: N must be a multiple of 16 (32 when gated)", op);
+  STRIX_REQUIRE(m.top_k >= 1, "%s: top_k must be >= 1", op);
+  STRIX_REQUIRE(m.num_blocks * m.block_m >= m.sorted_len, "%s: expert_ids.numel() * block_m must cover sorted_ids", op);
+  STRIX_REQUIRE(m.lda >= m.K && m.lda % 8 == 0 && aligned(m.a, 16), "%s: activation rows must be >= K, 16-byte aligned", op);
+  const int64_t n_out = m.silu_mul ? m.N / 2 : m.N;
+  STRIX_REQUIRE(m.ldc >= n_out && m.ldc % 4 == 0 && aligned(m.c, 8), "%s: output rows must be >= %lld, 8-byte aligned", op,
+                (long long)n_out);
+  STRIX_REQUIRE(m.activation == kActSilu || m.activation == kActGeluTanh, "%s: unknown activation", op);
+  STRIX_REQUIRE(aligned(p.w, 16) && p.ldw % 16 == 0, "%s: weight rows must be 16-byte aligned", op);
+  int rc = check_scale_kind(op, p.ws_kind);
+  if (rc) return rc;
+  if (m.num_blocks == 0 || m.num_slots == 0 || m.N == 0) return STRIX_OK;
+  STRIX_ARCH_GATE();
+  p.a = static_cast<const uint16_t*>(m.a); p.lda = m.lda;
+  p.out = m.c; p.ldo = m.ldc; p.out_f16 = m.c_dtype == STRIX_F16;
+  p.M = (int)m.num_slots; p.N = (int)m.N; p.K = (int)m.K; p.n_out = (int)n_out; p.gate_off = (int)(m.N / 2);
+  p.sorted_ids = m.sorted_ids; p.sorted_len = m.sorted_len; p.expert_ids = m.expert_ids; p.num_post = m.num_post;
+  p.num_slots = (int)m.num_slots; p.top_k = (int)m.top_k; p.topk_w = m.topk_w;
+  hipStream_t st = as_stream(stream);
+  const int nb = (int)m.num_blocks, bm = (int)m.block_m;
+  const bool f16 = m.a_dtype == STRIX_F16;
+  if (m.silu_mul) {
+    if (m.activation == kActGeluTanh)
+      return f16 ? moe16_dispatch<FMT, kEpiGated, kActGeluTanh, true>(p, bm, nb, st, op)
+                 : moe16_dispatch<FMT, kEpiGated, kActGeluTanh, false>(p, bm, nb, st, op);
+    return f16 ? moe16_dispatch<FMT, kEpiGated, kActSilu, true>(p, bm, nb, st, op)
+               : moe16_dispatch<FMT, kEpiGated, kActSilu, false>(p, bm, nb, st, op);
+  }
+  return f16 ? moe16_dispatch<FMT, kEpiStore, kActSilu, true>(p, bm, nb, st, op)
+             : moe16_dispatch<FMT, kEpiStore, kActSilu, false>(p, bm, nb, st, op);
+}
+
+template <int FMT>
+int run_dense16(const char* op, G16 p, const void* x, int x_dtype, int64_t ldx, void* out, int64_t ldo, int out_dtype,
+                int64_t M, int64_t N, int64_t K, int cfg, void* stream) {
+  STRIX_REQUIRE(x_dtype == STRIX_BF16 || x_dtype == STRIX_F16, "%s: activations must be bfloat16 or float16", op);
+  STRIX_REQUIRE(out_dtype == STRIX_BF16 || out_dtype == STRIX_F16, "%s: output must be bfloat16 or float16", op);
+  STRIX_REQUIRE(M >= 0 && N >= 0 && K >= 0, "%s: negative size", op);
+  STRIX_REQUIRE(ldx >= K && ldx % 8 == 0 && aligned(x, 16), "%s: activation rows must be >= K, 16-byte aligned", op);
+  STRIX_REQUIRE(ldo >= N && ldo % 4 == 0 && aligned(out, 8), "%s: output rows must be >= N, 8-byte aligned", op);
+  STRIX_REQUIRE(aligned(p.w, 16) && p.ldw % 16 == 0, "%s: weight rows must be 16-byte aligned", op);
+  STRIX_REQUIRE(M <= INT32_MAX && N <= INT32_MAX && K <= INT32_MAX, "%s: sizes overflow 32-bit indexing", op);
+  int rc = check_scale_kind(op, p.ws_kind);
+  if (rc) return rc;
+  if (M == 0 || N == 0) return STRIX_OK;
+  STRIX_ARCH_GATE();
+  p.a = static_cast<const uint16_t*>(x); p.lda = ldx;
+  p.out = out; p.ldo = ldo; p.out_f16 = out_dtype == STRIX_F16;
+  p.M = (int)M; p.N = (int)N; p.K = (int)K; p.n_out = (int)N;
+  hipStream_t st = as_stream(stream);
+  return x_dtype == STRIX_F16 ? dense16_dispatch<FMT, true>(p, st, op, cfg) : dense16_dispatch<FMT, false>(p, st, op, cfg);
+}
+
+G16 g16_weights(const void* w, int64_t w_es, int64_t ldw, const void* s, int s_kind, int64_t s_es, int64_t s_ns,
+                int64_t s_ks, int kgroup, int nblock) {
+  G16 p = {};
+  p.w = static_cast<const uint8_t*>(w); p.w_es = w_es; p.ldw = ldw;
+  p.ws = s; p.ws_kind = s_kind; p.ws_es = s_es; p.ws_ns = s_ns; p.ws_ks = s_ks; p.ws_kgroup = kgroup;
+  p.ws_nblock = nblock;
+  return p;
+}
+
+}  // namespace
+}  // namespace strix
+
+using namespace strix;
+
+extern "C" {
+
+#define STRIX_MOE16_ARGS STRIX_MOE16_PARAMS
+#define STRIX_MOE16_PACK                                                                                            \
+  MoeArgs m{c, ldc, c_dtype, a, lda, a_dtype, sorted_ids, sorted_len, expert_ids, num_blocks, num_post, topk_weights, \
+            num_slots, top_k, block_m, silu_mul, activation, N, K}
+
+int strix_moe_gemm_mxfp4(const uint8_t* w, int64_t w_es, int64_t ldw, const uint8_t* scales, int64_t s_es, int64_t s_ns,
+                         STRIX_MOE16_ARGS) {
+  STRIX_MOE16_PACK;
+  const char* op = "moe_gemm_mxfp4";
+  STRIX_REQUIRE(ldw * 2 >= K, "%s: weight rows must hold K/2 bytes", op);
+  return run_moe16<kWMxfp4>(op, m, g16_weights(w, w_es, ldw, scales, kSE8m0, s_es, s_ns, 1, 32, 1), stream);
+}
+
+int strix_moe_gemm_w4a16_zp(const uint8_t* w, int64_t w_es, int64_t ldw, const void* scales, int s_kind, int64_t s_es,
+                            int64_t s_ns, const uint8_t* zeros, int64_t z_es, int64_t z_ns, int64_t group,
+                            STRIX_MOE16_ARGS) {
+  STRIX_MOE16_PACK;
+  const char* op = "moe_gemm_w4a16_zp";
+  STRIX_REQUIRE(group == 32 || group == 64 || group == 128, "%s: group_size must be 32, 64 or 128", op);
+  STRIX_REQUIRE(K % group == 0, "%s: K must be a multiple of group_size", op);
+  STRIX_REQUIRE(s_kind == kSBf16 || s_kind == kSF16 || s_kind == kSF32, "%s: scales must be bf16, fp16 or fp32", op);
+  G16 p = g16_weights(w, w_es, ldw, scales, s_kind, s_es, s_ns, 1, (int)group, 1);
+  p.wz = zeros; p.wz_es = z_es; p.wz_ns = z_ns; p.wz_ks = 1;
+  return run_moe16<kWInt4Zp>(op, m, p, stream);
+}
+
+int strix_moe_gemm_w4a16(const uint8_t* w, int64_t w_es, int64_t ldw, const void* scales, int s_kind, int64_t s_es,
+                         int64_t s_ns, int64_t group, STRIX_MOE16_ARGS) {
+  STRIX_MOE16_PACK;
+  const char* op = "moe_gemm_w4a16";
+  STRIX_REQUIRE(group == 32 || group == 64 || group == 128, "%s: group_size must be 32, 64 or 128", op);
+  STRIX_REQUIRE(s_kind == kSBf16 || s_kind == kSF16 || s_kind == kSF32, "%s: scales must be bf16, fp16 or fp32", op);
+  return run_moe16<kWInt4Sym>(op, m, g16_weights(w, w_es, ldw, scales, s_kind, s_es, s_ns, 1, (int)group, 1), stream);
+}
+
+int strix_moe_gemm_bf16(const uint16_t* w, int64_t w_es, int64_t ldw, STRIX_MOE16_ARGS) {
+  STRIX_MOE16_PACK;
+  // ldw in elements for the bf16 layout; the kernels use byte strides.
+  return run_moe16<kWBf16>("moe_gemm_bf16", m, g16_weights(w, w_es * 2, ldw * 2, nullptr, kSF32, 0, 0, 0, 0, 1), stream);
+}
+
+// fp8 weights, W8A16: block scales [E][N/128][K/128] (nblock 128, kgroup 128) or per channel [E][N] (kgroup 0).
+int strix_moe_gemm_fp8_w8a16(const uint8_t* w, int64_t w_es, int64_t ldw, const void* scales, int s_kind, int64_t s_es,
+                             int64_t s_ns, int64_t s_ks, int block_scales, STRIX_MOE16_ARGS) {
+  STRIX_MOE16_PACK;
+  const char* op = "moe_gemm_fp8";
+  STRIX_REQUIRE(!block_scales || (K % 128 == 0), "%s: K must be a multiple of 128 with block scales", op);
+  G16 p = block_scales ? g16_weights(w, w_es, ldw, scales, s_kind, s_es, s_ns, s_ks, 128, 128)
+                       : g16_weights(w, w_es, ldw, scales, s_kind, s_es, s_ns, 0, 0, 1);
+  return run_moe16<kWFp8>(op, m, p, stream);
+}
+
+int strix_moe_gemm_w8a16(const int8_t* w, int64_t w_es, int64_t ldw, const void* scales, int s_kind, int64_t s_es,
+                         int64_t s_ns, STRIX_MOE16_ARGS) {
+  STRIX_MOE16_PACK;
+  return run_moe16<kWInt8>("moe_gemm_w8a16", m, g16_weights(w, w_es, ldw, scales, s_kind, s_es, s_ns, 0, 0, 1), stream);
+}
+
+// Dense MXFP4 W4A16 (mxfp4_wmma_gemm): w [N, ldw >= K/2] u8, scales e8m0 [N, s_ld], bias (may be NULL).
+int strix_mxfp4_gemm(const uint8_t* w, int64_t ldw, const uint8_t* scales, int64_t s_ld, const void* x, int x_dtype,
+                     int64_t ldx, const void* bias, int64_t bias_rs, void* out, int64_t ldo, int out_dtype, int64_t M,
+                     int64_t N, int64_t K, int cfg, void* stream) {
+  const char* op = "mxfp4_wmma_gemm";
+  STRIX_REQUIRE(K % 64 == 0, "%s: K must be a multiple of 64, got K=%lld", op, (long long)K);
+  G16 p = g16_weights(w, 0, ldw, scales, kSE8m0, 0, s_ld, 1, 32, 1);
+  p.bias = static_cast<const uint16_t*>(bias);
+  p.bias_rs = bias_rs;
+  return run_dense16<kWMxfp4>(op, p, x, x_dtype, ldx, out, ldo, out_dtype, M, N, K, cfg, stream);
+}
+
+// Dense FP8 W8A16 (fp8_wmma_gemm / _raw): bf16 or fp16 activations, block or channel scales.
+int strix_fp8_w8a16_gemm(const uint8_t* w, int64_t ldw, const float* scales, int64_t s_ld, int block_scales,
+                         const void* x, int x_dtype, int64_t ldx, void* out, int64_t ldo, int out_dtype, int64_t M,
+                         int64_t N, int64_t K, int cfg, void* stream) {
+  const char* op = "fp8_wmma_gemm";
+  STRIX_REQUIRE(K % 64 == 0, "%s: K must be a multiple of 64, got K=%lld", op, (long long)K);
+  STRIX_REQUIRE(!block_scales || K % 128 == 0, "%s: K must be a multiple of 128 with block scales", op);
+  G16 p = block_scales ? g16_weights(w, 0, ldw, scales, kSF32, 0, s_ld, 1, 128, 128)
+                       : g16_weights(w, 0, ldw, scales, kSF32, 0, 1, 0, 0, 1);
+  return run_dense16<kWFp8>(op, p, x, x_dtype, ldx, out, ldo, out_dtype, M, N, K, cfg, stream);
+}
+
+// Whole-matrix dequant to bf16: fmt 1 MXFP4 (e8m0 scales [N, s_ld]), 4 FP8 (block
+// scales [N/128, s_ld] or channel [N]), 3 INT4 symmetric plain nibbles (group g, scales [N, s_ld]).
+int strix_dequant_bf16(int fmt, const uint8_t* w, int64_t ldw, const void* scales, int s_kind, int64_t s_ld,
+                       int64_t kgroup, int64_t nblock, uint16_t* out, int64_t ldo, int64_t N, int64_t K, void* stream) {
+  const char* op = fmt == kWMxfp4 ? "mxfp4_dequant" : (fmt == kWFp8 ? "fp8_dequant" : "w4a16_dequant");
+  STRIX_REQUIRE(fmt == kWMxfp4 || fmt == kWFp8 || fmt == kWInt4Sym, "%s: unsupported format %d", op, fmt);
+  const int bits = fmt == kWFp8 ? 8 : 4;
+  const int pv = 128 / bits;
+  STRIX_REQUIRE(K % pv == 0, "%s: K must be a multiple of %d", op, pv);
+  STRIX_REQUIRE(aligned(w, 16) && ldw % 16 == 0 && aligned(out, 16) && ldo % 8 == 0, "%s: rows must be 16-byte aligned", op);
+  int rc = check_scale_kind(op, s_kind);
+  if (rc) return rc;
+  if (N == 0 || K == 0) return STRIX_OK;
+  STRIX_ARCH_GATE();
+  G16 p = g16_weights(w, 0, ldw, scales, s_kind, 0, s_ld, 1, (int)kgroup, (int)nblock);
+  if (kgroup == 0) p.ws_ns = s_ld;  // per-channel: one scale per row (s_ld = stride between rows)
+  p.N = (int)N;
+  p.K = (int)K;
+  const int64_t pieces = N * (K / pv);
+  const unsigned blocks = (unsigned)((pieces + 255) / 256);
+  hipStream_t st = as_stream(stream);
+  if (fmt == kWMxfp4) hipLaunchKernelGGL(dequant_kernel<kWMxfp4>, dim3(blocks), dim3(256), 0, st, p, out, ldo);
+  else if (fmt == kWFp8) hipLaunchKernelGGL(dequant_kernel<kWFp8>, dim3(blocks), dim3(256), 0, st, p, out, ldo);
+  else hipLaunchKernelGGL(dequant_kernel<kWInt4Sym>, dim3(blocks), dim3(256), 0, st, p, out, ldo);
+  return check_launch(op);
+}
+
+}  // extern "C"

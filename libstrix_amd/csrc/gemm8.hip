@@ -20,13 +20,13 @@
 //            staging) into a fragment-native layout, two LDS stages of 128 K,
 //            conflict-free ds_read_b128 fragment reads. Prefill.
 #include "capi_internal.h"
+#include "gemm_common.h"
 #include "strix_common.h"
 
 namespace strix {
 namespace {
 
 enum Kind8 : int { kFp8Block = 0, kI8Token = 1, kI8Group = 2 };
-enum Epi : int { kEpiStore = 0, kEpiGated = 1, kEpiI32 = 2 };
 
 struct G8 {
   const uint8_t* w;  // weight bytes [E][N][ldw]
@@ -51,20 +51,6 @@ struct G8 {
   const float* topk_w;
 };
 
-__device__ __forceinline__ u32x4 ldg128(const uint8_t* p) {
-  return *reinterpret_cast<const u32x4*>(p);
-}
-__device__ __forceinline__ u32x4 lds128(const uint8_t* p) {
-  return *reinterpret_cast<const u32x4*>(p);
-}
-__device__ __forceinline__ v8i cat8(const u32x4& lo, const u32x4& hi) {
-  v8i r;
-  r[0] = lo[0]; r[1] = lo[1]; r[2] = lo[2]; r[3] = lo[3];
-  r[4] = hi[0]; r[5] = hi[1]; r[6] = hi[2]; r[7] = hi[3];
-  return r;
-}
-__device__ __forceinline__ v4i lo4(const v8i& x) { v4i r; r[0] = x[0]; r[1] = x[1]; r[2] = x[2]; r[3] = x[3]; return r; }
-__device__ __forceinline__ v4i hi4(const v8i& x) { v4i r; r[0] = x[4]; r[1] = x[5]; r[2] = x[6]; r[3] = x[7]; return r; }
 __device__ __forceinline__ v8i flip80(const v8i& x) {
   v8i r;
 #pragma unroll
@@ -72,54 +58,9 @@ __device__ __forceinline__ v8i flip80(const v8i& x) {
   return r;
 }
 
-// Token row of MFMA column m (block-relative index already added).
-template <bool MOE>
-__device__ __forceinline__ void token_row(const G8& p, int m, int& brow, int& orow, bool& valid) {
-  if constexpr (MOE) {
-    const int sid = (m < p.sorted_len) ? p.sorted_ids[m] : p.num_slots;
-    valid = sid >= 0 && sid < p.num_slots;
-    brow = valid ? sid / p.top_k : 0;
-    orow = sid;
-  } else {
-    valid = m < p.M;
-    brow = valid ? m : 0;
-    orow = m;
-  }
-}
-
-// Stores four consecutive output columns col0..col0+3 of row orow.
-__device__ __forceinline__ void store4(const G8& p, int orow, int col0, const float v[4]) {
-  if (p.out_f16) {
-    uint16_t* o = static_cast<uint16_t*>(p.out) + (int64_t)orow * p.ldo + col0;
-    if (col0 + 3 < p.n_out) {
-      *reinterpret_cast<uint2*>(o) = make_uint2(f32_to_f16_bits(v[0]) | (f32_to_f16_bits(v[1]) << 16),
-                                                f32_to_f16_bits(v[2]) | (f32_to_f16_bits(v[3]) << 16));
-    } else {
-      for (int i = 0; i < 4; ++i)
-        if (col0 + i < p.n_out) o[i] = (uint16_t)f32_to_f16_bits(v[i]);
-    }
-  } else {
-    uint16_t* o = static_cast<uint16_t*>(p.out) + (int64_t)orow * p.ldo + col0;
-    if (col0 + 3 < p.n_out) {
-      *reinterpret_cast<uint2*>(o) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
-    } else {
-      for (int i = 0; i < 4; ++i)
-        if (col0 + i < p.n_out) o[i] = (uint16_t)f32_to_bf16_bits(v[i]);
-    }
-  }
-}
-__device__ __forceinline__ void store4_i32(const G8& p, int orow, int col0, const int v[4]) {
-  int* o = static_cast<int*>(p.out) + (int64_t)orow * p.ldo + col0;
-  if (col0 + 3 < p.n_out) {
-    *reinterpret_cast<int4*>(o) = make_int4(v[0], v[1], v[2], v[3]);
-  } else {
-    for (int i = 0; i < 4; ++i)
-      if (col0 + i < p.n_out) o[i] = v[i];
-  }
-}
-
 // Final epilogue for one output subtile: `g` holds the (gate) values, `u` the
-// up values when gated. I8 token values arrive as int32 bit patterns.
+// up values when gated. I8 token values arrive as int32 bit patterns and are
+// scaled here: (acc * sa[m]) * sw[n].
 template <int KIND, int EPI, int ACT, bool MOE>
 __device__ __forceinline__ void finish4(const G8& p, int orow, int brow, bool valid, int col0,
                                         const float g[4], const float u[4]) {
@@ -131,29 +72,18 @@ __device__ __forceinline__ void finish4(const G8& p, int orow, int brow, bool va
     store4_i32(p, orow, col0, iv);
     return;
   }
-  float v[4];
   if constexpr (KIND == kI8Token) {
     const float sa = p.sa[(int64_t)brow * p.sa_rs];
+    float v[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int n = min(col0 + i, p.N - 1);
       v[i] = ((float)__float_as_int(g[i]) * sa) * p.sw[(int64_t)n * p.sw_ns];
     }
-  } else if constexpr (EPI == kEpiGated) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = gate_act<ACT>(g[i]) * u[i];
+    finish_float4<kEpiStore, ACT, MOE>(p, orow, col0, v, u);
   } else {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = g[i];
+    finish_float4<EPI, ACT, MOE>(p, orow, col0, g, u);
   }
-  if constexpr (MOE) {
-    if (p.topk_w) {
-      const float tw = p.topk_w[orow];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] *= tw;
-    }
-  }
-  store4(p, orow, col0, v);
 }
 
 // ============================================================ stream8
@@ -345,18 +275,6 @@ __global__ void __launch_bounds__(WAVES * 64) stream8_kernel(G8 p) {
 // so a wave's outstanding copies retire strictly in issue order and
 // `s_waitcnt vmcnt(n)` with n = copies issued for later stages waits for
 // exactly one stage.
-// LDS row swizzle: chunk c of operand row r sits at slot c ^ lds_swz(r), so
-// the 16 lanes of a ds_read_b128 group (rows r..r+15, one chunk index) hit 16
-// distinct 16-byte bank groups.
-__device__ __forceinline__ int lds_swz(int row) { return (row >> 1) & 7; }
-
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit counter");
-  // gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]
-  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
-
 template <int KIND, int BM, int BN, int WM, int WN, int STAGES, bool MOE, int EPI, int ACT, bool WX128>
 __global__ void __launch_bounds__(WM * WN * 64) tiled8_kernel(G8 p, int tiles_m, int tiles_n, int group_m) {
   constexpr int W = WM * WN;
@@ -397,18 +315,7 @@ __global__ void __launch_bounds__(WM * WN * 64) tiled8_kernel(G8 p, int tiles_m,
     expert = p.expert_ids[tm];
     if (expert < 0) return;
   } else {
-    // XCD-aware order: the hardware deals block b to XCD b % 8; give each
-    // XCD a contiguous run of tiles, then walk them in group_m-tall columns.
-    const int nblk = tiles_m * tiles_n;
-    int b = blockIdx.x;
-    if ((nblk & 7) == 0) b = (b & 7) * (nblk >> 3) + (b >> 3);
-    const int per_group = group_m * tiles_n;
-    const int grp = b / per_group;
-    const int first_m = grp * group_m;
-    const int gm = min(tiles_m - first_m, group_m);
-    const int in = b - grp * per_group;
-    tm = first_m + in % gm;
-    tn = in / gm;
+    dense_tile(blockIdx.x, tiles_m, tiles_n, group_m, tm, tn);
   }
   const int m0 = tm * BM;
   auto wrow_of = [&](int j) -> int {  // first weight row of LDS weight subtile j

@@ -1,0 +1,131 @@
+// SPDX-License-Identifier: MIT
+// Pieces shared by the 8-bit (gemm8.hip) and 16-bit (gemm16.hip) GEMM
+// kernels: raw vector moves, the dense/MoE token-row mapping, the swizzled LDS
+// row layout and the epilogue (gated act*mul, top-k weight, bf16/fp16 store).
+//
+// MoE contract (reference: csrc/moe/moe_gemm_w8a16.hip:76-404,
+// tests/test_moe_gemm.py:9-42): sorted_ids groups slot ids by expert; a slot
+// id >= num_slots is padding; the A row of slot s is s / top_k; a block whose
+// first sorted position is >= num_post_padded, or whose expert id is < 0,
+// does nothing.
+#pragma once
+
+#include "strix_common.h"
+
+namespace strix {
+
+enum Epi : int { kEpiStore = 0, kEpiGated = 1, kEpiI32 = 2 };
+
+__device__ __forceinline__ u32x4 ldg128(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ __forceinline__ u32x4 lds128(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ __forceinline__ v8i cat8(const u32x4& lo, const u32x4& hi) {
+  v8i r;
+  r[0] = lo[0]; r[1] = lo[1]; r[2] = lo[2]; r[3] = lo[3];
+  r[4] = hi[0]; r[5] = hi[1]; r[6] = hi[2]; r[7] = hi[3];
+  return r;
+}
+__device__ __forceinline__ v4i lo4(const v8i& x) { v4i r; r[0] = x[0]; r[1] = x[1]; r[2] = x[2]; r[3] = x[3]; return r; }
+__device__ __forceinline__ v4i hi4(const v8i& x) { v4i r; r[0] = x[4]; r[1] = x[5]; r[2] = x[6]; r[3] = x[7]; return r; }
+
+// LDS operand rows are 128 bytes (8 chunks of 16 B). Chunk c of row r sits at
+// slot c ^ lds_swz(r), so the 16 lanes of one ds_read_b128 group (16
+// consecutive rows, one chunk index) hit 16 distinct 16-byte bank groups.
+__device__ __forceinline__ int lds_swz(int row) { return (row >> 1) & 7; }
+
+// Waits until at most N vector-memory operations of this wave are in flight.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit counter");
+  // gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Token row of MFMA column m (block-relative index already added): brow is
+// the activation row to read (a valid row even for padding), orow the output
+// row, valid whether the result is stored.
+template <bool MOE, class P>
+__device__ __forceinline__ void token_row(const P& p, int m, int& brow, int& orow, bool& valid) {
+  if constexpr (MOE) {
+    const int sid = (m < p.sorted_len) ? p.sorted_ids[m] : p.num_slots;
+    valid = sid >= 0 && sid < p.num_slots;
+    brow = valid ? sid / p.top_k : 0;
+    orow = sid;
+  } else {
+    valid = m < p.M;
+    brow = valid ? m : 0;
+    orow = m;
+  }
+}
+
+// Stores four consecutive output columns col0..col0+3 of row orow.
+template <class P>
+__device__ __forceinline__ void store4(const P& p, int orow, int col0, const float v[4]) {
+  uint16_t* o = static_cast<uint16_t*>(p.out) + (int64_t)orow * p.ldo + col0;
+  if (p.out_f16) {
+    if (col0 + 3 < p.n_out) {
+      *reinterpret_cast<uint2*>(o) = make_uint2(f32_to_f16_bits(v[0]) | (f32_to_f16_bits(v[1]) << 16),
+                                                f32_to_f16_bits(v[2]) | (f32_to_f16_bits(v[3]) << 16));
+    } else {
+      for (int i = 0; i < 4; ++i)
+        if (col0 + i < p.n_out) o[i] = (uint16_t)f32_to_f16_bits(v[i]);
+    }
+  } else {
+    if (col0 + 3 < p.n_out) {
+      *reinterpret_cast<uint2*>(o) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+    } else {
+      for (int i = 0; i < 4; ++i)
+        if (col0 + i < p.n_out) o[i] = (uint16_t)f32_to_bf16_bits(v[i]);
+    }
+  }
+}
+
+template <class P>
+__device__ __forceinline__ void store4_i32(const P& p, int orow, int col0, const int v[4]) {
+  int* o = static_cast<int*>(p.out) + (int64_t)orow * p.ldo + col0;
+  if (col0 + 3 < p.n_out) {
+    *reinterpret_cast<int4*>(o) = make_int4(v[0], v[1], v[2], v[3]);
+  } else {
+    for (int i = 0; i < 4; ++i)
+      if (col0 + i < p.n_out) o[i] = v[i];
+  }
+}
+
+// Float epilogue of one lane's four results: act(g)*u when gated, times the
+// slot's top-k weight (MoE, when given), then the store.
+template <int EPI, int ACT, bool MOE, class P>
+__device__ __forceinline__ void finish_float4(const P& p, int orow, int col0, const float g[4], const float u[4]) {
+  float v[4];
+  if constexpr (EPI == kEpiGated) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = gate_act<ACT>(g[i]) * u[i];
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = g[i];
+  }
+  if constexpr (MOE) {
+    if (p.topk_w) {
+      const float tw = p.topk_w[orow];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] *= tw;
+    }
+  }
+  store4(p, orow, col0, v);
+}
+
+// Maps a dense block index to (tile_m, tile_n): the hardware deals block b to
+// XCD b % 8, so each XCD gets a contiguous run of tiles, walked in
+// group_m-tall columns (tiles sharing a weight column run back to back).
+__device__ __forceinline__ void dense_tile(int bid, int tiles_m, int tiles_n, int group_m, int& tm, int& tn) {
+  const int nblk = tiles_m * tiles_n;
+  int b = bid;
+  if ((nblk & 7) == 0) b = (b & 7) * (nblk >> 3) + (b >> 3);
+  const int per_group = group_m * tiles_n;
+  const int grp = b / per_group;
+  const int first_m = grp * group_m;
+  const int gm = min(tiles_m - first_m, group_m);
+  const int in = b - grp * per_group;
+  tm = first_m + in % gm;
+  tn = in / gm;
+}
+
+}  // namespace strix

@@ -69,3 +69,48 @@ def fused_moe_fp8_w8a8(x, logits, w13, w13_s, w2, w2_s, top_k: int, renormalize:
     out = torch.empty((t, h), dtype=torch.bfloat16, device=x.device)
     S.moe_sum(y.view(t, top_k, h), out)
     return out
+
+
+def _fused_moe_16(x, logits, top_k, inter, hidden, num_experts, renormalize, activation, block_m, w13_call, w2_call):
+    """route -> align -> w13 (fused act*mul) -> w2 (x top-k weight) -> sum, bf16 activations throughout."""
+    t = x.size(0)
+    bm = block_m or moe_block_m(t, top_k, num_experts)
+    _, w, sorted_ids, expert_ids, num_post = route_and_align(logits, top_k, num_experts, bm, renormalize)
+    slots = t * top_k
+    h13 = torch.empty((slots, inter), dtype=x.dtype, device=x.device)
+    w13_call(h13, x, sorted_ids, expert_ids, num_post, None, top_k, bm, True, activation)
+    y = torch.empty((slots, hidden), dtype=x.dtype, device=x.device)
+    w2_call(y, h13, sorted_ids, expert_ids, num_post, w.reshape(-1), 1, bm, False, activation)
+    out = torch.empty((t, hidden), dtype=x.dtype, device=x.device)
+    S.moe_sum(y.view(t, top_k, hidden), out)
+    return out
+
+
+def fused_moe_mxfp4(x, logits, w13, w13_s, w2, w2_s, top_k: int, renormalize: bool = True,
+                    activation: str = "silu", block_m: int | None = None):
+    """MXFP4 W4A16 fused MoE (config 4): e2m1 + e8m0 experts decoded to bf16 in LDS, bf16 MFMA."""
+    e, n13, _ = w13.shape
+    hidden = w2.size(1)
+
+    def g13(c, a, si, ei, npp, tw, k, bm, silu, act):
+        S.moe_gemm_mxfp4(c, a, w13, w13_s, si, ei, npp, tw, k, bm, 64, silu, act)
+
+    def g2(c, a, si, ei, npp, tw, k, bm, silu, act):
+        S.moe_gemm_mxfp4(c, a, w2, w2_s, si, ei, npp, tw, k, bm, 64, silu, act)
+
+    return _fused_moe_16(x, logits, top_k, n13 // 2, hidden, e, renormalize, activation, block_m, g13, g2)
+
+
+def fused_moe_wna16(x, logits, w13, w13_s, w13_z, w2, w2_s, w2_z, top_k: int, group: int = 128,
+                    renormalize: bool = True, activation: str = "silu", block_m: int | None = None):
+    """WNA16 int4 fused MoE with zero points (config 5): (q - z) * s decoded to bf16 in LDS, bf16 MFMA."""
+    e, n13, _ = w13.shape
+    hidden = w2.size(1)
+
+    def g13(c, a, si, ei, npp, tw, k, bm, silu, act):
+        S.moe_gemm_w4a16_zp(c, a, w13, w13_s, w13_z, si, ei, npp, tw, k, bm, 64, silu, act, group)
+
+    def g2(c, a, si, ei, npp, tw, k, bm, silu, act):
+        S.moe_gemm_w4a16_zp(c, a, w2, w2_s, w2_z, si, ei, npp, tw, k, bm, 64, silu, act, group)
+
+    return _fused_moe_16(x, logits, top_k, n13 // 2, hidden, e, renormalize, activation, block_m, g13, g2)

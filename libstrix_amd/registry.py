@@ -209,6 +209,126 @@ KERNELS: list[Kernel] = [
          "quant": "fp8_w8a8"},
         _MOE_TILES,
     ),
+    # ------------------------------------------------ 16-bit MFMA over dequantized weights
+    Kernel(
+        "moe_gemm_mxfp4",
+        "moe_gemm_mxfp4",
+        "MXFP4 expert GEMM: e2m1 nibbles [E, N, K/2] (low nibble = even k) with e8m0 [E, N, K/32] decoded "
+        "exactly to bf16 once per block into LDS, bf16 16x16x32 MFMA, bf16 activations (W4A16); fused "
+        "act*mul (w13) or top-k weight (w2). K % 64 == 0 (2880 is fine), ragged N",
+        {"silu_mul": (True, False), "dtype": "bf16", "weight_dtype": "uint8", "weight_bits": 4, "quant": "mxfp4",
+         "group_size": 32, "activation": ("silu", "gelu_tanh")},
+        _MOE_TILES,
+    ),
+    Kernel(
+        "moe_gemm_w4a16_zp",
+        "moe_gemm_w4a16",
+        "WNA16 expert GEMM with zero points (AWQ-style): uint4 [E, N, K/8] int32 words (k = 8w + j in "
+        "nibble j), bf16/fp16 scales and uint4 zero points [E, N/2, K/G]; (q - z) * s decoded to bf16 in LDS",
+        {"silu_mul": (True, False), "dtype": "bf16", "weight_bits": 4, "quant": "wna16", "has_zp": True,
+         "group_size": (32, 64, 128), "activation": ("silu", "gelu_tanh")},
+        _MOE_TILES,
+    ),
+    Kernel(
+        "moe_gemm_w4a16",
+        "moe_gemm_w4a16",
+        "WNA16 symmetric expert GEMM over vLLM's Triton layout: uint8 [E, N, K/2] (low nibble = even k), "
+        "(q - 8) * s decoded to bf16 in LDS",
+        {"silu_mul": (True, False), "dtype": "bf16", "weight_dtype": "uint8", "weight_bits": 4, "quant": "wna16",
+         "has_zp": False, "group_size": (32, 64, 128), "activation": ("silu", "gelu_tanh")},
+        _MOE_TILES,
+    ),
+    Kernel(
+        "moe_gemm_bf16",
+        "moe_gemm",
+        "unquantized bf16 expert GEMM: both operands by direct global->LDS copy, bf16 MFMA, same fused "
+        "epilogues",
+        {"silu_mul": (True, False), **_BF16, "weight_dtype": "bf16", "quant": "none",
+         "activation": ("silu", "gelu_tanh")},
+        _MOE_TILES,
+    ),
+    Kernel(
+        "moe_gemm_w8a16",
+        "moe_gemm_w8a16",
+        "int8 experts [E, N, K] with per-channel scales ([E, N] or [E, N, 1]), int8 * scale decoded to bf16 in "
+        "LDS, bf16 activations (W8A16)",
+        {"silu_mul": (True, False), **_BF16, "weight_dtype": "int8", "weight_bits": 8, "quant": "int8",
+         "group_size": (0,), "activation": ("silu", "gelu_tanh")},
+        _MOE_TILES,
+    ),
+    Kernel(
+        "moe_gemm_fp8",
+        "moe_gemm_fp8",
+        "e4m3 experts with 128x128 block scales [E, N/128, K/128] or per-channel scales, decoded with the "
+        "scale to bf16 in LDS, bf16 activations (W8A16)",
+        {"silu_mul": (True, False), **_BF16, "weight_dtype": "fp8_e4m3", "weight_bits": 8, "quant": "fp8",
+         "group_size": (0, 128), "activation": ("silu", "gelu_tanh")},
+        _MOE_TILES,
+    ),
+    Kernel(
+        "moe_gemm_fp8_raw",
+        "moe_gemm_fp8",
+        "the same with fp16 activations: weights decoded to fp16, f16 MFMA; fp16 or bf16 output (the c tensor's "
+        "dtype)",
+        {"silu_mul": (True, False), "dtype": "fp16", "weight_dtype": "fp8_e4m3", "weight_bits": 8, "quant": "fp8",
+         "group_size": (0, 128), "activation": ("silu", "gelu_tanh")},
+        _MOE_TILES,
+    ),
+    Kernel(
+        "mxfp4_wmma_gemm",
+        "mxfp4",
+        "dense MXFP4 W4A16: packed e2m1 [N, K/2] + e8m0 [N, K/32], read in place (decode in registers for "
+        "M <= 64, decoded into LDS once per block otherwise), bf16 MFMA, optional [N] or [M, N] bias. K % 64 == 0",
+        {"weight_bits": 4, "group_size": 32, "dtype": ("bf16", "fp16"), "scale_dtype": "e8m0"},
+        {"tiles": "stream 16/32/64 rows, tiled 128x128"},
+    ),
+    Kernel(
+        "mxfp4_wmma_gemm_cfg",
+        "mxfp4_tile_sweep",
+        "mxfp4_wmma_gemm pinned to one tile config: 0 stream16 | 1 stream32 | 2 stream64 | 3 tiled 128x128 | "
+        "4 tiled 256x128 | 5 tiled 64x128",
+        {"weight_bits": 4, "group_size": 32, "dtype": ("bf16", "fp16")},
+    ),
+    Kernel(
+        "mxfp4_dequant",
+        "mxfp4_dequant",
+        "MXFP4 [N, K/2] + e8m0 [N, K/32] -> bf16 [N, K], exact (e2m1 times a power of two), zero blocks for "
+        "an e8m0 byte of 0",
+        {"weight_bits": 4, "group_size": 32, "dtype": "bf16"},
+        {"threads": 256},
+    ),
+    Kernel(
+        "fp8_wmma_gemm",
+        "fp8",
+        "dense FP8 W8A16: e4m3 [N, K] with 128x128 block or per-channel scales decoded to bf16, bf16 MFMA",
+        {"weight_bits": 8, "weight_dtype": "fp8_e4m3", "group_size": (0, 128), "rows": Range(lo=1), "dtype": "bf16"},
+    ),
+    Kernel(
+        "fp8_wmma_gemm_raw",
+        "fp8",
+        "dense FP8 W8A16 with fp16 activations: e4m3 decoded with its scale to fp16, f16 MFMA, bf16 output",
+        {"weight_bits": 8, "weight_dtype": "fp8_e4m3", "group_size": (0, 128), "rows": Range(lo=1), "dtype": "fp16"},
+    ),
+    Kernel(
+        "fp8_wmma_gemm_cfg",
+        "fp8_tile_sweep",
+        "fp8_wmma_gemm pinned to one tile config (0..5)",
+        {"weight_bits": 8, "weight_dtype": "fp8_e4m3", "group_size": (0, 128), "dtype": "bf16"},
+    ),
+    Kernel(
+        "fp8_wmma_gemm_raw_cfg",
+        "fp8_tile_sweep",
+        "fp8_wmma_gemm_raw pinned to one tile config (0..5)",
+        {"weight_bits": 8, "weight_dtype": "fp8_e4m3", "group_size": (0, 128), "dtype": "fp16"},
+    ),
+    Kernel(
+        "fp8_dequant",
+        "fp8_dequant",
+        "float8_e4m3fn [N, K] + 128x128 block or per-channel scales -> bf16 [N, K] (exact decode, one "
+        "rounding at the scale multiply)",
+        {"weight_bits": 8, "weight_dtype": "fp8_e4m3", "group_size": (0, 128), "dtype": "bf16"},
+        {"threads": 256},
+    ),
 ]
 
 _selections: dict[tuple, dict[str, Any]] = {}

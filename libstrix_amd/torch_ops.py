@@ -420,3 +420,376 @@ def _g2l_probe(src):
 @_fake("_g2l_probe")
 def _(src):
     return torch.empty_like(src)
+
+
+# ----------------------------------------------------------------- 16-bit MFMA over dequantized weights
+_SCALE_KIND = {torch.float32: _lib.S_F32, torch.bfloat16: _lib.S_BF16, torch.float16: _lib.S_F16}
+
+
+def _moe16_tail(c, a, sorted_ids, expert_ids, num_post_padded, topk_weights, top_k, block_m, silu_mul, activation,
+                n, k):
+    _check(c.dim() == 2 and c.stride(1) == 1 and c.dtype in (torch.bfloat16, torch.float16), "c must be bf16/fp16 2-D")
+    _check(a.dim() == 2 and a.stride(1) == 1 and a.size(1) == k, f"a must be [rows, K={k}] and contiguous in dim 1")
+    _moe_common(c, sorted_ids, expert_ids, num_post_padded, topk_weights, block_m)
+    return [_ptr(c), c.stride(0), _out_code(c.dtype), _ptr(a), a.stride(0), _act_code(a), _ptr(sorted_ids),
+            sorted_ids.numel(), _ptr(expert_ids), expert_ids.numel(), _ptr(num_post_padded), _ptr(topk_weights),
+            c.size(0), top_k, block_m, int(bool(silu_mul)), _activation(activation), n, k, _stream(c)]
+
+
+def _expert_stack(b, what):
+    _check(b.dim() == 3 and b.stride(2) == 1, f"{what} must be [E, N, K'] and contiguous in the last dim")
+
+
+@_define(
+    "moe_gemm_mxfp4(Tensor(a!) c, Tensor a, Tensor b, Tensor scales, Tensor sorted_ids, Tensor expert_ids, "
+    "Tensor num_post_padded, Tensor? topk_weights, int top_k, int block_m, int block_n, bool silu_mul=False, "
+    "str activation='silu') -> ()"
+)
+def moe_gemm_mxfp4(c, a, b, scales, sorted_ids, expert_ids, num_post_padded, topk_weights, top_k, block_m, block_n,
+                   silu_mul=False, activation="silu"):
+    _expert_stack(b, "b")
+    _check(b.dtype == torch.uint8, "b must be uint8 packed e2m1 [E, N, K/2]")
+    _check(scales.dtype == torch.uint8, "scale must be uint8 (e8m0)")
+    e, n, k2 = b.shape
+    k = 2 * k2
+    _check(tuple(scales.shape) == (e, n, k // 32) and scales.stride(2) == 1, "scales must be e8m0 [E, N, K/32]")
+    tail = _moe16_tail(c, a, sorted_ids, expert_ids, num_post_padded, topk_weights, top_k, block_m, silu_mul,
+                       activation, n, k)
+    _lib.call("strix_moe_gemm_mxfp4", _ptr(b), b.stride(0), b.stride(1), _ptr(scales), scales.stride(0),
+              scales.stride(1), *tail)
+
+
+@_fake("moe_gemm_mxfp4")
+def _(c, a, b, scales, sorted_ids, expert_ids, num_post_padded, topk_weights, top_k, block_m, block_n,
+      silu_mul=False, activation="silu"):
+    return None
+
+
+def _int4_bytes(b):
+    """int32 [E, N, K/8] or uint8 [E, N, K/2] packed int4 -> the uint8 view."""
+    if b.dtype == torch.int32:
+        return b.view(torch.uint8)
+    _check(b.dtype == torch.uint8, "b must be int32 [E, N, K/8] or uint8 [E, N, K/2] packed int4")
+    return b
+
+
+@_define(
+    "moe_gemm_w4a16_zp(Tensor(a!) c, Tensor a, Tensor b, Tensor scales, Tensor zeros, Tensor sorted_ids, "
+    "Tensor expert_ids, Tensor num_post_padded, Tensor? topk_weights, int top_k, int block_m, int block_n, "
+    "bool silu_mul=False, str activation='silu', int group_size=128) -> ()"
+)
+def moe_gemm_w4a16_zp(c, a, b, scales, zeros, sorted_ids, expert_ids, num_post_padded, topk_weights, top_k, block_m,
+                      block_n, silu_mul=False, activation="silu", group_size=128):
+    _expert_stack(b, "b")
+    bu = _int4_bytes(b)
+    e, n, k2 = bu.shape
+    k = 2 * k2
+    _check(scales.dtype in (torch.bfloat16, torch.float16) and tuple(scales.shape) == (e, n, k // group_size)
+           and scales.stride(2) == 1, "scales must be bf16/fp16 [E, N, K/group_size]")
+    _check(zeros.dtype == torch.uint8 and tuple(zeros.shape) == (e, n // 2, k // group_size) and zeros.stride(2) == 1,
+           "zeros must be uint8 [E, N/2, K/group_size] (two uint4 zero points per byte along N)")
+    tail = _moe16_tail(c, a, sorted_ids, expert_ids, num_post_padded, topk_weights, top_k, block_m, silu_mul,
+                       activation, n, k)
+    _lib.call("strix_moe_gemm_w4a16_zp", _ptr(bu), bu.stride(0), bu.stride(1), _ptr(scales), _SCALE_KIND[scales.dtype],
+              scales.stride(0), scales.stride(1), _ptr(zeros), zeros.stride(0), zeros.stride(1), group_size, *tail)
+
+
+@_fake("moe_gemm_w4a16_zp")
+def _(c, a, b, scales, zeros, sorted_ids, expert_ids, num_post_padded, topk_weights, top_k, block_m, block_n,
+      silu_mul=False, activation="silu", group_size=128):
+    return None
+
+
+# Reference schema: csrc/torch_ops.cpp:191-195.
+@_define(
+    "moe_gemm_w4a16(Tensor(a!) c, Tensor a, Tensor b, Tensor scales, "
+    "Tensor sorted_ids, Tensor expert_ids, Tensor num_post_padded, "
+    "Tensor? topk_weights, int top_k, int block_m, int block_n, "
+    "bool silu_mul=False, str activation='silu', int group_size=32) -> ()"
+)
+def moe_gemm_w4a16(c, a, b, scales, sorted_ids, expert_ids, num_post_padded, topk_weights, top_k, block_m, block_n,
+                   silu_mul=False, activation="silu", group_size=32):
+    _expert_stack(b, "b")
+    bu = _int4_bytes(b)
+    e, n, k2 = bu.shape
+    k = 2 * k2
+    _check(scales.dtype in (torch.bfloat16, torch.float16, torch.float32)
+           and tuple(scales.shape) == (e, n, k // group_size) and scales.stride(2) == 1,
+           "scales must be [E, N, K/group_size]")
+    _check(n % block_n == 0, f"N={n} is not a multiple of block_n={block_n}")
+    tail = _moe16_tail(c, a, sorted_ids, expert_ids, num_post_padded, topk_weights, top_k, block_m, silu_mul,
+                       activation, n, k)
+    _lib.call("strix_moe_gemm_w4a16", _ptr(bu), bu.stride(0), bu.stride(1), _ptr(scales), _SCALE_KIND[scales.dtype],
+              scales.stride(0), scales.stride(1), group_size, *tail)
+
+
+@_fake("moe_gemm_w4a16")
+def _(c, a, b, scales, sorted_ids, expert_ids, num_post_padded, topk_weights, top_k, block_m, block_n,
+      silu_mul=False, activation="silu", group_size=32):
+    return None
+
+
+# Reference schema: csrc/torch_ops.cpp:185-189.
+@_define(
+    "moe_gemm_bf16(Tensor(a!) c, Tensor a, Tensor b, Tensor sorted_ids, "
+    "Tensor expert_ids, Tensor num_post_padded, Tensor? topk_weights, "
+    "int top_k, int block_m, int block_n, bool silu_mul=False, "
+    "str activation='silu') -> ()"
+)
+def moe_gemm_bf16(c, a, b, sorted_ids, expert_ids, num_post_padded, topk_weights, top_k, block_m, block_n,
+                  silu_mul=False, activation="silu"):
+    _expert_stack(b, "b")
+    _check(b.dtype == a.dtype == torch.bfloat16, "a and b must be bfloat16")
+    e, n, k = b.shape
+    _check(n % block_n == 0, f"N={n} is not a multiple of block_n={block_n}")
+    tail = _moe16_tail(c, a, sorted_ids, expert_ids, num_post_padded, topk_weights, top_k, block_m, silu_mul,
+                       activation, n, k)
+    _lib.call("strix_moe_gemm_bf16", _ptr(b), b.stride(0), b.stride(1), *tail)
+
+
+@_fake("moe_gemm_bf16")
+def _(c, a, b, sorted_ids, expert_ids, num_post_padded, topk_weights, top_k, block_m, block_n, silu_mul=False,
+      activation="silu"):
+    return None
+
+
+def _channel_scales(scales, e, n):
+    """[E, N] or [E, N, 1] per-channel scales -> (tensor, expert stride, row stride)."""
+    _check(scales.dim() in (2, 3) and scales.size(0) == e and scales.size(1) == n
+           and (scales.dim() == 2 or scales.size(2) == 1), f"scales must be [E, N] or [E, N, 1], E={e}, N={n}")
+    _check(scales.dtype in _SCALE_KIND, "scales must be float32, bfloat16 or float16")
+    return scales, scales.stride(0), scales.stride(1)
+
+
+def _moe_fp8_w8a16(c, a, b, scales, sorted_ids, expert_ids, num_post_padded, topk_weights, top_k, block_m, block_n,
+                   silu_mul, activation):
+    _expert_stack(b, "b")
+    _check(b.dtype == torch.float8_e4m3fn, "b must be float8_e4m3fn [E, N, K]")
+    e, n, k = b.shape
+    _check(n % block_n == 0, f"N={n} is not a multiple of block_n={block_n}")
+    block = scales.dim() == 3 and tuple(scales.shape) == (e, (n + 127) // 128, k // 128) and scales.size(2) != 1
+    if block:
+        _check(scales.dtype == torch.float32 and scales.stride(2) == 1, "block scales must be float32 [E, N/128, K/128]")
+        s_es, s_ns, s_ks = scales.stride(0), scales.stride(1), scales.stride(2)
+    else:
+        scales, s_es, s_ns = _channel_scales(scales, e, n)
+        s_ks = 0
+    tail = _moe16_tail(c, a, sorted_ids, expert_ids, num_post_padded, topk_weights, top_k, block_m, silu_mul,
+                       activation, n, k)
+    _lib.call("strix_moe_gemm_fp8_w8a16", _ptr(b), b.stride(0), b.stride(1), _ptr(scales), _SCALE_KIND[scales.dtype],
+              s_es, s_ns, s_ks, int(block), *tail)
+
+
+# Reference schemas: csrc/torch_ops.cpp:225-232 (W8A16: bf16 or fp16 "raw" activations).
+@_define(
+    "moe_gemm_fp8(Tensor(a!) c, Tensor a, Tensor b, Tensor scales, "
+    "Tensor sorted_ids, Tensor expert_ids, Tensor num_post_padded, "
+    "Tensor? topk_weights, int top_k, int block_m, int block_n, "
+    "bool silu_mul=False, str activation='silu') -> ()"
+)
+def moe_gemm_fp8(c, a, b, scales, sorted_ids, expert_ids, num_post_padded, topk_weights, top_k, block_m, block_n,
+                 silu_mul=False, activation="silu"):
+    _check(a.dtype == torch.bfloat16, "a must be bfloat16 (moe_gemm_fp8_raw takes float16)")
+    _moe_fp8_w8a16(c, a, b, scales, sorted_ids, expert_ids, num_post_padded, topk_weights, top_k, block_m, block_n,
+                   silu_mul, activation)
+
+
+@_fake("moe_gemm_fp8")
+def _(c, a, b, scales, sorted_ids, expert_ids, num_post_padded, topk_weights, top_k, block_m, block_n,
+      silu_mul=False, activation="silu"):
+    return None
+
+
+@_define(
+    "moe_gemm_fp8_raw(Tensor(a!) c, Tensor a, Tensor b, Tensor scales, "
+    "Tensor sorted_ids, Tensor expert_ids, Tensor num_post_padded, "
+    "Tensor? topk_weights, int top_k, int block_m, int block_n, "
+    "bool silu_mul=False, str activation='silu') -> ()"
+)
+def moe_gemm_fp8_raw(c, a, b, scales, sorted_ids, expert_ids, num_post_padded, topk_weights, top_k, block_m, block_n,
+                     silu_mul=False, activation="silu"):
+    _check(a.dtype == torch.float16, "a must be float16")
+    _moe_fp8_w8a16(c, a, b, scales, sorted_ids, expert_ids, num_post_padded, topk_weights, top_k, block_m, block_n,
+                   silu_mul, activation)
+
+
+@_fake("moe_gemm_fp8_raw")
+def _(c, a, b, scales, sorted_ids, expert_ids, num_post_padded, topk_weights, top_k, block_m, block_n,
+      silu_mul=False, activation="silu"):
+    return None
+
+
+# Reference schema: csrc/torch_ops.cpp:221-224 (int8 experts, per-channel scales).
+@_define(
+    "moe_gemm_w8a16(Tensor(a!) c, Tensor a, Tensor b, Tensor scales, "
+    "Tensor sorted_ids, Tensor expert_ids, Tensor num_post_padded, "
+    "Tensor? topk_weights, int top_k, int block_m, int block_n, "
+    "bool silu_mul=False, str activation='silu') -> ()"
+)
+def moe_gemm_w8a16(c, a, b, scales, sorted_ids, expert_ids, num_post_padded, topk_weights, top_k, block_m, block_n,
+                   silu_mul=False, activation="silu"):
+    _expert_stack(b, "b")
+    _check(b.dtype == torch.int8, "b must be int8 [E, N, K]")
+    e, n, k = b.shape
+    _check(n % block_n == 0, f"N={n} is not a multiple of block_n={block_n}")
+    scales, s_es, s_ns = _channel_scales(scales, e, n)
+    tail = _moe16_tail(c, a, sorted_ids, expert_ids, num_post_padded, topk_weights, top_k, block_m, silu_mul,
+                       activation, n, k)
+    _lib.call("strix_moe_gemm_w8a16", _ptr(b), b.stride(0), b.stride(1), _ptr(scales), _SCALE_KIND[scales.dtype], s_es,
+              s_ns, *tail)
+
+
+@_fake("moe_gemm_w8a16")
+def _(c, a, b, scales, sorted_ids, expert_ids, num_post_padded, topk_weights, top_k, block_m, block_n,
+      silu_mul=False, activation="silu"):
+    return None
+
+
+# ----------------------------------------------------------------- dense MXFP4 / FP8 W8A16
+def _mxfp4_dense(w, x, scales, bias, cfg):
+    _check(w.dim() == 2 and x.dim() == 2, "w must be [N, K/2] and x [M, K]")
+    n, k = w.size(0), x.size(1)
+    _check(w.dtype == torch.uint8 and w.stride(1) == 1 and 2 * w.size(1) == k, "w must be uint8 [N, K/2]")
+    _check(scales.dtype == torch.uint8, "scale must be uint8 (e8m0)")
+    _check(k % 64 == 0, f"K must be a multiple of 64, got K={k}")
+    _check(tuple(scales.shape) == (n, k // 32) and scales.stride(1) == 1, "scales must be [N, K/32]")
+    _check(x.dtype in (torch.bfloat16, torch.float16) and x.stride(1) == 1, "x must be bf16/fp16, contiguous in dim 1")
+    m = x.size(0)
+    out = torch.empty((m, n), dtype=x.dtype, device=x.device)
+    bias_rs = 0
+    if bias is not None:
+        _check(bias.dtype == x.dtype, "bias must have the activation dtype")
+        if bias.dim() == 2:
+            _check(tuple(bias.shape) == (m, n) and bias.stride(1) == 1, "bias must be [N] or [M, N]")
+            bias_rs = bias.stride(0)
+        else:
+            _check(bias.numel() == n, "bias must be [N] or [M, N]")
+            bias = bias.contiguous()
+    _lib.call("strix_mxfp4_gemm", _ptr(w), w.stride(0), _ptr(scales), scales.stride(0), _ptr(x), _act_code(x),
+              x.stride(0), _ptr(bias), bias_rs, _ptr(out), n, _act_code(out), m, n, k, cfg, _stream(x))
+    return out
+
+
+# Reference schemas: csrc/torch_ops.cpp:283-292.
+@_define("mxfp4_wmma_gemm(Tensor w, Tensor x, Tensor scales, Tensor? bias) -> Tensor")
+def mxfp4_wmma_gemm(w, x, scales, bias):
+    return _mxfp4_dense(w, x, scales, bias, -1)
+
+
+@_fake("mxfp4_wmma_gemm")
+def _(w, x, scales, bias):
+    return x.new_empty((x.size(0), w.size(0)))
+
+
+@_define("mxfp4_wmma_gemm_cfg(Tensor w, Tensor x, Tensor scales, Tensor? bias, int cfg) -> Tensor")
+def mxfp4_wmma_gemm_cfg(w, x, scales, bias, cfg):
+    return _mxfp4_dense(w, x, scales, bias, int(cfg))
+
+
+@_fake("mxfp4_wmma_gemm_cfg")
+def _(w, x, scales, bias, cfg):
+    return x.new_empty((x.size(0), w.size(0)))
+
+
+@_define("mxfp4_dequant(Tensor w, Tensor scales) -> Tensor")
+def mxfp4_dequant(w, scales):
+    _check(w.dim() == 2 and w.dtype == torch.uint8 and w.stride(1) == 1, "w must be uint8 [N, K/2]")
+    _check(scales.dtype == torch.uint8, "scale must be uint8 (e8m0)")
+    n, k = w.size(0), 2 * w.size(1)
+    _check(tuple(scales.shape) == (n, k // 32) and scales.stride(1) == 1, "scales must be [N, K/32]")
+    out = torch.empty((n, k), dtype=torch.bfloat16, device=w.device)
+    _lib.call("strix_dequant_bf16", _lib.FMT_MXFP4, _ptr(w), w.stride(0), _ptr(scales), _lib.S_E8M0, scales.stride(0),
+              32, 1, _ptr(out), k, n, k, _stream(w))
+    return out
+
+
+@_fake("mxfp4_dequant")
+def _(w, scales):
+    return w.new_empty((w.size(0), w.size(1) * 2), dtype=torch.bfloat16)
+
+
+def _fp8_scales_dense(scales, n, k):
+    """128x128 block scales [ceil(N/128), K/128] or per-channel [N] (fp32)."""
+    _check(scales.dtype == torch.float32, f"scales must be float32, got {scales.dtype}")
+    if scales.dim() == 2 and tuple(scales.shape) == ((n + 127) // 128, k // 128) and scales.stride(1) == 1:
+        _check(k % 128 == 0, f"K must be a multiple of 128 with block scales, got K={k}")
+        return True, scales.stride(0)
+    _check(scales.numel() == n, f"scales must be [ceil(N/128), K/128] block or [N] channel scales, got "
+           f"{list(scales.shape)}")
+    return False, 1
+
+
+def _fp8_w8a16(w, x, scales, raw, cfg):
+    _check(w.dim() == 2 and x.dim() == 2, "w must be [N, K] and x [M, K]")
+    _check(w.dtype == torch.float8_e4m3fn and w.stride(1) == 1, "w must be float8_e4m3fn [N, K], contiguous in dim 1")
+    n, k = w.shape
+    _check(x.size(1) == k, f"x K ({x.size(1)}) must match w K ({k})")
+    _check(x.dtype == (torch.float16 if raw else torch.bfloat16), f"x must be {'float16' if raw else 'bfloat16'}")
+    _check(x.stride(1) == 1, "x must be contiguous in dim 1")
+    block, s_ld = _fp8_scales_dense(scales, n, k)
+    if not block:
+        scales = scales.contiguous()
+    m = x.size(0)
+    out = torch.empty((m, n), dtype=torch.bfloat16, device=x.device)
+    _lib.call("strix_fp8_w8a16_gemm", _ptr(w), w.stride(0), _ptr(scales), s_ld, int(block), _ptr(x), _act_code(x),
+              x.stride(0), _ptr(out), n, _lib.BF16, m, n, k, cfg, _stream(x))
+    return out
+
+
+# Reference schemas: csrc/torch_ops.cpp:253-256.
+@_define("fp8_wmma_gemm(Tensor w, Tensor x, Tensor scales) -> Tensor")
+def fp8_wmma_gemm(w, x, scales):
+    return _fp8_w8a16(w, x, scales, False, -1)
+
+
+@_fake("fp8_wmma_gemm")
+def _(w, x, scales):
+    return x.new_empty((x.size(0), w.size(0)))
+
+
+@_define("fp8_wmma_gemm_cfg(Tensor w, Tensor x, Tensor scales, int cfg) -> Tensor")
+def fp8_wmma_gemm_cfg(w, x, scales, cfg):
+    return _fp8_w8a16(w, x, scales, False, int(cfg))
+
+
+@_fake("fp8_wmma_gemm_cfg")
+def _(w, x, scales, cfg):
+    return x.new_empty((x.size(0), w.size(0)))
+
+
+@_define("fp8_wmma_gemm_raw(Tensor w, Tensor x, Tensor scales) -> Tensor")
+def fp8_wmma_gemm_raw(w, x, scales):
+    return _fp8_w8a16(w, x, scales, True, -1)
+
+
+@_fake("fp8_wmma_gemm_raw")
+def _(w, x, scales):
+    return x.new_empty((x.size(0), w.size(0)), dtype=torch.bfloat16)
+
+
+@_define("fp8_wmma_gemm_raw_cfg(Tensor w, Tensor x, Tensor scales, int cfg) -> Tensor")
+def fp8_wmma_gemm_raw_cfg(w, x, scales, cfg):
+    return _fp8_w8a16(w, x, scales, True, int(cfg))
+
+
+@_fake("fp8_wmma_gemm_raw_cfg")
+def _(w, x, scales, cfg):
+    return x.new_empty((x.size(0), w.size(0)), dtype=torch.bfloat16)
+
+
+@_define("fp8_dequant(Tensor w, Tensor scales) -> Tensor")
+def fp8_dequant(w, scales):
+    _check(w.dim() == 2 and w.dtype == torch.float8_e4m3fn and w.stride(1) == 1, "w must be float8_e4m3fn [N, K]")
+    n, k = w.shape
+    block, s_ld = _fp8_scales_dense(scales, n, k)
+    if not block:
+        scales = scales.contiguous()
+    out = torch.empty((n, k), dtype=torch.bfloat16, device=w.device)
+    _lib.call("strix_dequant_bf16", _lib.FMT_FP8, _ptr(w), w.stride(0), _ptr(scales), _lib.S_F32, s_ld,
+              128 if block else 0, 128 if block else 1, _ptr(out), k, n, k, _stream(w))
+    return out
+
+
+@_fake("fp8_dequant")
+def _(w, scales):
+    return w.new_empty((w.size(0), w.size(1)), dtype=torch.bfloat16)
