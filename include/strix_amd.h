@@ -176,6 +176,11 @@ int strix_moe_sum(const void* y, int dtype, int64_t ldy, int64_t T, int64_t top_
 int strix_probe_mfma(int kind, const void* a, const void* b, void* d, int64_t K, void* stream);
 /* global_load_lds_dwordx4 placement: dst = src with its 64 16-byte chunks reversed. */
 int strix_probe_g2l(const uint8_t* src, uint8_t* dst, void* stream);
+/* Hardware converters: fp4_out [nscales][4 byte lanes][256 bytes][2] bf16 bits of
+ * v_cvt_scalef32_pk_bf16_fp4; fp8_out [256] of v_cvt_pk_f32_fp8; bf16_out[i] =
+ * v_cvt_pk_bf16_f32(bf16_in[i]). */
+int strix_probe_cvt(const float* scales, int64_t nscales, uint16_t* fp4_out, float* fp8_out, uint16_t* bf16_out,
+                    const float* bf16_in, int64_t nbf16, void* stream);
 
 #ifdef __cplusplus
 }

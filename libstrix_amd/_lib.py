@@ -58,6 +58,7 @@ SIGNATURES: dict[str, list] = {
     "strix_moe_sum": [P, I, L, L, L, L, P, P, L, P],
     "strix_probe_mfma": [I, P, P, P, L, P],
     "strix_probe_g2l": [P, P, P],
+    "strix_probe_cvt": [P, L, P, P, P, P, L, P],
 }
 _RESTYPE = {
     "strix_last_error": c_char_p,

@@ -115,3 +115,45 @@ int strix_probe_g2l(const uint8_t* src, uint8_t* dst, void* stream) {
 }
 
 }  // extern "C"
+
+// Conversion probes: what gfx950's converters produce, pinned against the
+// format definitions by tests (they decide which decoders the GEMMs may use).
+namespace strix {
+namespace {
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// out[s][b][j] (bf16 bits), j = 0,1: v_cvt_scalef32_pk_bf16_fp4 of byte b
+// (placed in byte lane `sel` of the source dword) with scale scales[s].
+template <int SEL>
+__device__ void cvt_fp4_one(uint32_t b, float sc, uint16_t* o) {
+  const bf16x2_t r = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(b << (8 * SEL), sc, SEL);
+  o[0] = __builtin_bit_cast(uint16_t, r[0]);
+  o[1] = __builtin_bit_cast(uint16_t, r[1]);
+}
+__global__ void probe_cvt_kernel(const float* scales, int nscales, uint16_t* fp4_out, float* fp8_out,
+                                 uint16_t* bf16_out, const float* bf16_in, int nbf16) {
+  const int b = threadIdx.x;  // 0..255
+  for (int s = 0; s < nscales; ++s) {
+    uint16_t* o = fp4_out + ((int64_t)s * 4 * 256 + b) * 2;
+    cvt_fp4_one<0>(b, scales[s], o);
+    cvt_fp4_one<1>(b, scales[s], o + 256 * 2);
+    cvt_fp4_one<2>(b, scales[s], o + 2 * 256 * 2);
+    cvt_fp4_one<3>(b, scales[s], o + 3 * 256 * 2);
+  }
+  // v_cvt_pk_f32_fp8 on the low word: byte b in byte 0 and 0x00 in byte 1.
+  const f32x2_t f = __builtin_amdgcn_cvt_pk_f32_fp8((int)b, false);
+  fp8_out[b] = f[0];
+  for (int i = b; i < nbf16; i += 256) bf16_out[i] = __builtin_bit_cast(uint16_t, (__bf16)bf16_in[i]);
+}
+}  // namespace
+}  // namespace strix
+
+extern "C" int strix_probe_cvt(const float* scales, int64_t nscales, uint16_t* fp4_out, float* fp8_out,
+                               uint16_t* bf16_out, const float* bf16_in, int64_t nbf16, void* stream) {
+  STRIX_REQUIRE(nscales >= 1 && nscales <= 64, "probe_cvt: 1..64 scales");
+  STRIX_ARCH_GATE();
+  hipLaunchKernelGGL(strix::probe_cvt_kernel, dim3(1), dim3(256), 0, strix::as_stream(stream), scales, (int)nscales,
+                     fp4_out, fp8_out, bf16_out, bf16_in, (int)nbf16);
+  return strix::check_launch("probe_cvt");
+}

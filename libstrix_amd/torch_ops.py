@@ -793,3 +793,21 @@ def fp8_dequant(w, scales):
 @_fake("fp8_dequant")
 def _(w, scales):
     return w.new_empty((w.size(0), w.size(1)), dtype=torch.bfloat16)
+
+
+@_define("_cvt_probe(Tensor scales, Tensor bf16_in) -> (Tensor, Tensor, Tensor)")
+def _cvt_probe(scales, bf16_in):
+    _check(scales.dtype == torch.float32 and bf16_in.dtype == torch.float32, "float32 inputs")
+    s = scales.contiguous()
+    x = bf16_in.contiguous()
+    fp4 = torch.empty((s.numel(), 4, 256, 2), dtype=torch.int16, device=s.device)
+    fp8 = torch.empty((256,), dtype=torch.float32, device=s.device)
+    b16 = torch.empty((x.numel(),), dtype=torch.int16, device=s.device)
+    _lib.call("strix_probe_cvt", _ptr(s), s.numel(), _ptr(fp4), _ptr(fp8), _ptr(b16), _ptr(x), x.numel(), _stream(s))
+    return fp4, fp8, b16
+
+
+@_fake("_cvt_probe")
+def _(scales, bf16_in):
+    return (scales.new_empty((scales.numel(), 4, 256, 2), dtype=torch.int16), scales.new_empty((256,)),
+            bf16_in.new_empty((bf16_in.numel(),), dtype=torch.int16))
