@@ -19,6 +19,10 @@ int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3
 // 0 when the current device is gfx950, else an error (message set).
 int check_arch();
 
+// Compute units of the current device (cached; 256 if the query fails).
+// Called after check_arch() has passed.
+int cu_count();
+
 // Captures a launch error (if any) into the error slot.
 int check_launch(const char* what);
 

@@ -449,20 +449,33 @@ __global__ void __launch_bounds__(WM * WN * 64) tiled8_kernel(G8 p, int tiles_m,
 #pragma unroll
       for (int t = 0; t < MT; ++t) c1[t] = sw * sa_t[t];
     }
+    auto afrag = [&](int s) -> v8i {
+      const uint8_t* sub = st + aidx[s] * 2048;
+      return cat8(lds128(sub + frag0), lds128(sub + frag1));
+    };
+    // Software pipeline over the weight subtiles: the fragment of subtile
+    // s+1 is read while subtile s runs its MFMAs, and the block-scale fold
+    // of subtile s-1 is issued between them, so no fold waits on the MFMA
+    // that produced its operand. sched_barrier keeps each step's
+    // instructions in that step; the group barriers interleave one MFMA with
+    // the fold of one earlier result.
+    v8i afc = afrag(0);
+    v4f prev_f[MT];
+    v4i prev_i[MT];
+    float prev_sw[4];  // weight scale(s) of the previous subtile
 #pragma unroll
     for (int s = 0; s < NT; ++s) {
-      const uint8_t* sub = st + aidx[s] * 2048;
-      v8i af = cat8(lds128(sub + frag0), lds128(sub + frag1));
+      v8i afn;
+      if (s + 1 < NT) afn = afrag(s + 1);
+      v8i af = afc;
       if constexpr (WX128) af = flip80(af);
+      v4f part_f[MT];
+      v4i part_i[MT];
+      float cur_sw[4];
       if constexpr (KIND == kFp8Block) {
-        const float sw = ONE_SW ? 0.f : swl[aidx[s]];
+        cur_sw[0] = ONE_SW ? 0.f : swl[aidx[s]];
 #pragma unroll
-        for (int t = 0; t < MT; ++t) {
-          const v4f part = mfma_fp8(af, bf[t], v4f{0.f, 0.f, 0.f, 0.f});
-          const float c = ONE_SW ? c1[t] : sw * sa_t[t];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) acc[s][t][i] = fmaf(part[i], c, acc[s][t][i]);
-        }
+        for (int t = 0; t < MT; ++t) part_f[t] = mfma_fp8(af, bf[t], v4f{0.f, 0.f, 0.f, 0.f});
       } else if constexpr (KIND == kI8Token) {
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
@@ -470,17 +483,55 @@ __global__ void __launch_bounds__(WM * WN * 64) tiled8_kernel(G8 p, int tiles_m,
           acci[s][t] = mfma_i8(hi4(af), hi4(bf[t]), acci[s][t]);
         }
       } else {
-        float sw4[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sw4[i] = swl[16 * aidx[s] + 4 * g4 + i];
+        for (int i = 0; i < 4; ++i) cur_sw[i] = swl[16 * aidx[s] + 4 * g4 + i];
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
-          v4i part = mfma_i8(lo4(af), lo4(bf[t]), v4i{0, 0, 0, 0});
-          part = mfma_i8(hi4(af), hi4(bf[t]), part);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) acc[s][t][i] = fmaf((float)part[i], sw4[i] * sa_t[t], acc[s][t][i]);
+          part_i[t] = mfma_i8(lo4(af), lo4(bf[t]), v4i{0, 0, 0, 0});
+          part_i[t] = mfma_i8(hi4(af), hi4(bf[t]), part_i[t]);
         }
       }
+      // The fold's scale of subtile s' and token subtile t, row i of the lane's four.
+      auto fold_c = [&](const float* sw, int t, int i) -> float {
+        if constexpr (KIND == kFp8Block) return ONE_SW ? c1[t] : sw[0] * sa_t[t];
+        else return sw[i] * sa_t[t];
+      };
+      if constexpr (!INT_ACC) {
+        if (s > 0) {
+#pragma unroll
+          for (int t = 0; t < MT; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const float v = (KIND == kFp8Block) ? prev_f[t][i] : (float)prev_i[t][i];
+              acc[s - 1][t][i] = fmaf(v, fold_c(prev_sw, t, i), acc[s - 1][t][i]);
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          prev_f[t] = part_f[t];
+          prev_i[t] = part_i[t];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) prev_sw[i] = cur_sw[i];
+        if (s + 1 < NT) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          __builtin_amdgcn_sched_group_barrier(0x008, KIND == kFp8Block ? 1 : 2, 0);
+          if (s > 0) __builtin_amdgcn_sched_group_barrier(0x002, KIND == kFp8Block ? 4 : 8, 0);
+        }
+      }
+      if (s + 1 < NT) afc = afn;
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (!INT_ACC) {
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float v = (KIND == kFp8Block) ? prev_f[t][i] : (float)prev_i[t][i];
+          const float c = (KIND == kFp8Block) ? (ONE_SW ? c1[t] : prev_sw[0] * sa_t[t]) : prev_sw[i] * sa_t[t];
+          acc[NT - 1][t][i] = fmaf(v, c, acc[NT - 1][t][i]);
+        }
     }
   }
 
@@ -531,6 +582,43 @@ int launch_tiled(const G8& p, int grid_y_moe, hipStream_t st, const char* op) {
   return check_launch(op);
 }
 
+// The same dense GEMM restricted to output columns [n0, N): weights, weight
+// scales and output start n0 columns later.
+template <int KIND, int EPI>
+G8 dense_columns_from(const G8& p, int n0) {
+  G8 q = p;
+  q.w = p.w + (int64_t)n0 * p.ldw;
+  q.sw = p.sw + (KIND == kFp8Block ? (int64_t)(n0 / 128) * p.sw_ns : (int64_t)n0 * p.sw_ns);
+  q.out = static_cast<uint8_t*>(p.out) + (int64_t)n0 * (EPI == kEpiI32 ? 4 : 2);
+  q.N = p.N - n0;
+  q.n_out = p.n_out - n0;
+  return q;
+}
+
+// 256x256 tiles, one block per CU. When the tile count leaves a last round
+// less than half full, the whole rounds take the first columns and 128x128
+// tiles (a quarter of the work each) finish the remaining columns, so the
+// tail runs on every CU instead of a few.
+template <int KIND, int EPI, bool WX128>
+int launch_dense_256(const G8& p, hipStream_t st, const char* op) {
+  const int cus = cu_count();
+  const int tm = (p.M + 255) / 256, tn = (p.n_out + 255) / 256;
+  const int64_t tiles = (int64_t)tm * tn;
+  const int64_t rounds = tiles / cus, rem = tiles % cus;
+  if (rounds >= 1 && rem > 0 && 2 * rem <= cus) {
+    const int nb = (int)((rounds * cus) / tm);  // 256-column tiles run at full size
+    if (nb >= 1 && nb < tn) {
+      G8 big = p;
+      big.N = big.n_out = 256 * nb;
+      int rc = launch_tiled<KIND, 256, 256, 4, 2, 2, false, EPI, kActSilu, WX128>(big, 0, st, op);
+      if (rc) return rc;
+      return launch_tiled<KIND, 128, 128, 2, 2, 4, false, EPI, kActSilu, WX128>(
+          dense_columns_from<KIND, EPI>(p, 256 * nb), 0, st, op);
+    }
+  }
+  return launch_tiled<KIND, 256, 256, 4, 2, 2, false, EPI, kActSilu, WX128>(p, 0, st, op);
+}
+
 // Dense dispatch by M. cfg >= 0 pins one tile config (tile sweeps).
 template <int KIND, int EPI, bool WX128>
 int dense_dispatch(const G8& p, hipStream_t st, const char* op, int cfg) {
@@ -548,7 +636,7 @@ int dense_dispatch(const G8& p, hipStream_t st, const char* op, int cfg) {
     case 2: return launch_stream<KIND, 1, 4, 4, false, EPI, kActSilu, 2, WX128>(p, (M + 63) / 64, st, op);
     case 3: return launch_tiled<KIND, 128, 128, 2, 2, 4, false, EPI, kActSilu, WX128>(p, 0, st, op);
     case 4: return launch_tiled<KIND, 256, 64, 4, 2, 3, false, EPI, kActSilu, WX128>(p, 0, st, op);
-    case 5: return launch_tiled<KIND, 256, 256, 4, 2, 2, false, EPI, kActSilu, WX128>(p, 0, st, op);
+    case 5: return launch_dense_256<KIND, EPI, WX128>(p, st, op);
     case 6:
       // int8 group scales need one copy per 64 weight rows: 4 waves cannot carry 256 rows of them.
       if constexpr (KIND == kI8Group) return launch_tiled<KIND, 128, 128, 2, 2, 4, false, EPI, kActSilu, WX128>(p, 0, st, op);

@@ -8,6 +8,8 @@
 // host layer turns into a RuntimeError with the same text.
 #include <string.h>
 
+#include <atomic>
+
 #include "capi_internal.h"
 
 namespace strix {
@@ -22,24 +24,41 @@ int set_error(int code, const char* fmt, ...) {
   return code;
 }
 
+// Per-device facts, computed once (devices never change): arch verdict
+// (0 unknown, 1 gfx950, 2 other) and compute-unit count.
+static std::atomic<int> g_arch[64];
+static std::atomic<int> g_cus[64];
+
+static int query_device(int dev) {
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, dev) != hipSuccess)
+    return set_error(STRIX_ERR_DEVICE, "libstrix_amd: cannot query device %d", dev);
+  g_cus[dev].store(prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 1, std::memory_order_relaxed);
+  g_arch[dev].store(strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : 2, std::memory_order_release);
+  return STRIX_OK;
+}
+
 int check_arch() {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess)
     return set_error(STRIX_ERR_DEVICE, "libstrix_amd: no HIP device available");
-  // One answer per device, computed once (devices never change arch).
-  static int cached[64];  // 0 unknown, 1 gfx950, 2 other
   if (dev < 0 || dev >= 64)
     return set_error(STRIX_ERR_DEVICE, "libstrix_amd: device index %d out of range", dev);
-  if (cached[dev] == 0) {
-    hipDeviceProp_t prop;
-    if (hipGetDeviceProperties(&prop, dev) != hipSuccess)
-      return set_error(STRIX_ERR_DEVICE, "libstrix_amd: cannot query device %d", dev);
-    cached[dev] = strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : 2;
+  if (g_arch[dev].load(std::memory_order_acquire) == 0) {
+    int rc = query_device(dev);
+    if (rc != STRIX_OK) return rc;
   }
-  if (cached[dev] != 1)
+  if (g_arch[dev].load(std::memory_order_acquire) != 1)
     return set_error(STRIX_ERR_DEVICE,
                      "libstrix_amd targets gfx950 (MI355X, wave64 MFMA) GPUs only");
   return STRIX_OK;
+}
+
+int cu_count() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (g_arch[dev].load(std::memory_order_acquire) == 0 && query_device(dev) != STRIX_OK) return 256;
+  return g_cus[dev].load(std::memory_order_relaxed);
 }
 
 int check_launch(const char* what) {

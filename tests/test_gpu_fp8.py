@@ -54,6 +54,19 @@ def test_every_cfg(cfg):
     assert peak_rel_err(out, oracle.fp8_block_gemm(qa, sa, d["w"], d["sw"])) <= TOL
 
 
+def test_tail_split_columns():
+    """cfg 5 with more 256x256 tiles than one round: whole rounds take the
+    first columns, 128x128 tiles the rest (here a ragged 412-column strip)."""
+    m, n, k = 512, 33180, 256
+    d = workloads.c2_fp8(seed=11, m=m, n=n, k=k)
+    qa, sa = oracle.fp8_quant_group128(d["x"])
+    out = torch.ops.strix.fp8_w8a8_block_gemm_cfg(qa.to(DEV), sa.to(DEV), d["w"].to(DEV), d["sw"].to(DEV), 5).cpu()
+    rows = torch.cat([torch.arange(8), torch.arange(248, 264), torch.arange(m - 8, m)])
+    ref = oracle.fp8_block_gemm(qa[rows], sa[rows], d["w"], d["sw"])
+    assert peak_rel_err(out[rows], ref) <= TOL
+    assert peak_rel_err(out[rows, 32768:], ref[:, 32768:]) <= TOL
+
+
 def test_padded_weight_rows():
     d = workloads.c2_fp8(seed=5, m=40, n=512, k=1024)
     buf = torch.zeros(512, 1024 + 128, dtype=torch.uint8)

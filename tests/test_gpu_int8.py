@@ -59,6 +59,17 @@ def test_every_cfg_bit_exact(cfg):
     assert torch.equal(g.cpu(), oracle.w8a8_int8_gemm(q, s, d["w"], d["sw"]).to(torch.bfloat16))
 
 
+def test_tail_split_columns_bit_exact():
+    """cfg 5 past one round of 256x256 tiles: the 128x128 tail strip (ragged
+    240 columns) must give the same bits as the oracle too."""
+    m, n, k = 768, 22000, 256
+    d, q, s = _case(m, n, k, seed=12)
+    g = torch.ops.strix.w8a8_scaled_mm_cfg(q.to(DEV), s.to(DEV), d["w"].to(DEV), d["sw"].to(DEV), 5).cpu()
+    rows = torch.cat([torch.arange(4), torch.arange(254, 258), torch.arange(m - 4, m)])
+    ref = oracle.w8a8_int8_gemm(q[rows], s[rows], d["w"], d["sw"]).to(torch.bfloat16)
+    assert torch.equal(g[rows], ref)
+
+
 def test_extreme_accumulator():
     q = torch.full((16, 5120), 127, dtype=torch.int8)
     w = torch.full((32, 5120), -127, dtype=torch.int8)
