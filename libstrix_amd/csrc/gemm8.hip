@@ -87,12 +87,32 @@ __device__ __forceinline__ void finish4(const G8& p, int orow, int brow, bool va
 }
 
 // ============================================================ stream8
-template <int KIND, int NT, int MT, int WAVES, bool MOE, int EPI, int ACT, int U, bool WX128>
-__global__ void __launch_bounds__(WAVES * 64) stream8_kernel(G8 p) {
+// Decode-shaped GEMM straight from global memory into MFMA registers.
+// A block is 4 waves: NS = 4/KS groups of NT 16-row weight subtiles, each
+// group's K range split over KS waves (reduced through LDS). Each wave
+// streams its K range with a double-buffered register pipeline: the loads of
+// batch j+1 (U K-steps of weights, tokens and scales) are in flight while
+// batch j runs its MFMAs, so a wave keeps U..2U K-steps outstanding for its
+// whole life. Waves are independent streams, so the grid needs no rounds:
+// with KS = 1 every 16-row subtile is one long-lived wave.
+template <int NT, int MT>
+struct Frag8 {
+  v8i af[NT];
+  v8i bf[MT];
+  float sw[NT][4];
+  float sa[MT];
+};
+
+template <int KIND, int NT, int MT, int KS, bool MOE, int EPI, int ACT, int U, bool WX128, bool TOKL>
+__global__ void __launch_bounds__(256) stream8_kernel(G8 p) {
+  static_assert(!TOKL || MT == 1, "LDS token staging holds one 16-row token subtile");
+  constexpr int NS = 4 / KS;
+  static_assert(NS * KS == 4, "4 waves per block");
   constexpr int NTH = (EPI == kEpiGated) ? NT / 2 : NT;  // output subtiles
   constexpr bool INT_ACC = (KIND == kI8Token);
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int ks = wave % KS, ns = wave / KS;
   const int r16 = lane & 15, g4 = lane >> 4;
   const int m0 = blockIdx.y * (16 * MT);
   int expert = 0;
@@ -101,7 +121,8 @@ __global__ void __launch_bounds__(WAVES * 64) stream8_kernel(G8 p) {
     expert = p.expert_ids[blockIdx.y];
     if (expert < 0) return;
   }
-  const int nout0 = blockIdx.x * (16 * NTH);
+  const int nout0 = (blockIdx.x * NS + ns) * (16 * NTH);
+  const bool has_cols = nout0 < p.n_out;  // waves past the last subtile still take part in the reduction
 
   int wrow0[NT];  // first weight row of each subtile
 #pragma unroll
@@ -129,10 +150,23 @@ __global__ void __launch_bounds__(WAVES * 64) stream8_kernel(G8 p) {
     sap[t] = p.sa + (int64_t)brow[t] * p.sa_rs;
   }
   const float* swb = p.sw + (int64_t)expert * p.sw_es;
+  const float* swp[NT][4];  // weight-scale row pointers (fp8: one per subtile; int8 group: per lane row)
+#pragma unroll
+  for (int s = 0; s < NT; ++s)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      // fp8: one scale per 128-row block; the subtile's 16 rows share it, but
+      // the per-lane row keeps it a vector load (a scalar load here would be
+      // waited for as soon as it is issued).
+      if constexpr (KIND == kFp8Block)
+        swp[s][i] = swb + (int64_t)(min(wrow0[s] + r16, p.N - 1) >> 7) * p.sw_ns;
+      else
+        swp[s][i] = swb + (int64_t)min(wrow0[s] + 4 * g4 + i, p.N - 1) * p.sw_ns;
+    }
 
   const int nks = p.K >> 7;
-  const int per = (nks + WAVES - 1) / WAVES;
-  const int kb0 = min(nks, wave * per), kb1 = min(nks, kb0 + per);
+  const int per = (nks + KS - 1) / KS;
+  const int kb0 = min(nks, ks * per), kb1 = min(nks, kb0 + per);
 
   v4f acc[NT][MT];
   v4i acci[NT][MT];
@@ -144,83 +178,126 @@ __global__ void __launch_bounds__(WAVES * 64) stream8_kernel(G8 p) {
       acci[s][t] = v4i{0, 0, 0, 0};
     }
 
-  auto step = [&](int kb, const v8i (&af)[NT], const v8i (&bf)[MT]) {
-    if constexpr (KIND == kFp8Block) {
-      float sc_sw[NT];
+  // TOKL: the block's 16 token rows live in LDS for the whole K ([row][K]
+  // bytes, 16-byte chunks XOR-swizzled by row inside each 128-byte group so
+  // the fragment reads of 16 rows hit distinct banks); the register pipeline
+  // then carries weights and scales only.
+  extern __shared__ __attribute__((aligned(16))) uint8_t tok[];
+  const int tok_rows = MOE ? 16 : min(16, p.M - m0);  // rows staged (dense: the valid ones)
+  const int tok_r = r16 < tok_rows ? r16 : 0;           // row a lane reads
+  const uint8_t* tok_lane = tok + (int64_t)tok_r * p.K;
+
+  using F = Frag8<NT, MT>;
+  auto load = [&](int kb, F& f) {
+    const int64_t ko = (int64_t)kb * 128;
 #pragma unroll
-      for (int s = 0; s < NT; ++s) sc_sw[s] = swb[(int64_t)(wrow0[s] >> 7) * p.sw_ns + (int64_t)kb * p.sw_ks];
-      float sc_sa[MT];
+    for (int s = 0; s < NT; ++s) f.af[s] = cat8(ldg128(wp[s] + ko), ldg128(wp[s] + ko + 64));
+    if constexpr (!TOKL) {
 #pragma unroll
-      for (int t = 0; t < MT; ++t) sc_sa[t] = sap[t][(int64_t)kb * p.sa_ks];
+      for (int t = 0; t < MT; ++t) f.bf[t] = cat8(ldg128(ap[t] + ko), ldg128(ap[t] + ko + 64));
+    }
+    if constexpr (KIND != kI8Token) {
+#pragma unroll
+      for (int t = 0; t < MT; ++t) f.sa[t] = sap[t][(int64_t)kb * p.sa_ks];
 #pragma unroll
       for (int s = 0; s < NT; ++s)
 #pragma unroll
-        for (int t = 0; t < MT; ++t) {
-          const v4f part = mfma_fp8(af[s], bf[t], v4f{0.f, 0.f, 0.f, 0.f});
-          const float c = sc_sw[s] * sc_sa[t];
+        for (int i = 0; i < (KIND == kFp8Block ? 1 : 4); ++i) f.sw[s][i] = swp[s][i][(int64_t)kb * p.sw_ks];
+    }
+  };
+  auto step = [&](int kb, F& f) {
+    if constexpr (TOKL) {
+      const uint8_t* base = tok_lane + kb * 128;
+      f.bf[0] = cat8(lds128(base + 16 * (g4 ^ (tok_r & 7))), lds128(base + 16 * ((4 + g4) ^ (tok_r & 7))));
+    }
+#pragma unroll
+    for (int s = 0; s < NT; ++s) {
+      v8i af = f.af[s];
+      if constexpr (WX128) af = flip80(af);
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        if constexpr (KIND == kFp8Block) {
+          const v4f part = mfma_fp8(af, f.bf[t], v4f{0.f, 0.f, 0.f, 0.f});
+          const float c = f.sw[s][0] * f.sa[t];
 #pragma unroll
           for (int i = 0; i < 4; ++i) acc[s][t][i] = fmaf(part[i], c, acc[s][t][i]);
-        }
-    } else if constexpr (KIND == kI8Token) {
+        } else if constexpr (KIND == kI8Token) {
+          acci[s][t] = mfma_i8(lo4(af), lo4(f.bf[t]), acci[s][t]);
+          acci[s][t] = mfma_i8(hi4(af), hi4(f.bf[t]), acci[s][t]);
+        } else {
+          v4i part = mfma_i8(lo4(af), lo4(f.bf[t]), v4i{0, 0, 0, 0});
+          part = mfma_i8(hi4(af), hi4(f.bf[t]), part);
 #pragma unroll
-      for (int s = 0; s < NT; ++s)
-#pragma unroll
-        for (int t = 0; t < MT; ++t) {
-          acci[s][t] = mfma_i8(lo4(af[s]), lo4(bf[t]), acci[s][t]);
-          acci[s][t] = mfma_i8(hi4(af[s]), hi4(bf[t]), acci[s][t]);
-        }
-    } else {  // kI8Group
-      float sc_sa[MT];
-#pragma unroll
-      for (int t = 0; t < MT; ++t) sc_sa[t] = sap[t][(int64_t)kb * p.sa_ks];
-#pragma unroll
-      for (int s = 0; s < NT; ++s) {
-        float sw4[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int n = min(wrow0[s] + 4 * g4 + i, p.N - 1);
-          sw4[i] = swb[(int64_t)n * p.sw_ns + (int64_t)kb * p.sw_ks];
-        }
-#pragma unroll
-        for (int t = 0; t < MT; ++t) {
-          v4i part = mfma_i8(lo4(af[s]), lo4(bf[t]), v4i{0, 0, 0, 0});
-          part = mfma_i8(hi4(af[s]), hi4(bf[t]), part);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) acc[s][t][i] = fmaf((float)part[i], sw4[i] * sc_sa[t], acc[s][t][i]);
+          for (int i = 0; i < 4; ++i) acc[s][t][i] = fmaf((float)part[i], f.sw[s][i] * f.sa[t], acc[s][t][i]);
         }
       }
     }
   };
 
-  auto load = [&](int kb, v8i (&af)[NT], v8i (&bf)[MT]) {
-    const int64_t ko = (int64_t)kb * 128;
-#pragma unroll
-    for (int s = 0; s < NT; ++s) {
-      af[s] = cat8(ldg128(wp[s] + ko), ldg128(wp[s] + ko + 64));
-      if constexpr (WX128) af[s] = flip80(af[s]);
-    }
-#pragma unroll
-    for (int t = 0; t < MT; ++t) bf[t] = cat8(ldg128(ap[t] + ko), ldg128(ap[t] + ko + 64));
-  };
-
+  // Double-buffered batches, unrolled by two so the buffers never move. No
+  // load sits under a branch that skips it on one path: a join of "issued"
+  // and "not issued" paths would make every later wait a full vmcnt(0).
+  const int nb = (kb1 - kb0) / U;  // whole batches
   int kb = kb0;
-  for (; kb + U <= kb1; kb += U) {
-    v8i af[U][NT], bf[U][MT];
+  F fa[U], fb[U];
+  if (nb >= 1) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) load(kb + u, af[u], bf[u]);
+    for (int u = 0; u < U; ++u) load(kb + u, fa[u]);
+  }
+  if constexpr (TOKL) {
+    // Stage the token rows while the first weight batch is in flight.
+    const int chunks = p.K >> 4;
+    for (int idx = threadIdx.x; idx < tok_rows * chunks; idx += 256) {
+      const int row = idx / chunks, c = idx - row * chunks;
+      int br, orw;
+      bool v;
+      token_row<MOE>(p, m0 + row, br, orw, v);
+      const u32x4 x = ldg128(p.a + (int64_t)br * p.lda + 16 * c);
+      const int pos = (c & ~7) | ((c & 7) ^ (row & 7));
+      *reinterpret_cast<u32x4*>(tok + (int64_t)row * p.K + 16 * pos) = x;
+    }
+    __syncthreads();
+  }
+  if (nb >= 1) {
+    int j = 0;
+    for (; j + 2 < nb; j += 2) {  // batches j (in fa) and j+1 (in fb), and j+2 follows
 #pragma unroll
-    for (int u = 0; u < U; ++u) step(kb + u, af[u], bf[u]);
+      for (int u = 0; u < U; ++u) load(kb + U + u, fb[u]);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < U; ++u) step(kb + u, fa[u]);
+#pragma unroll
+      for (int u = 0; u < U; ++u) load(kb + 2 * U + u, fa[u]);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < U; ++u) step(kb + U + u, fb[u]);
+      kb += 2 * U;
+    }
+    if (j + 1 < nb) {  // two batches left
+#pragma unroll
+      for (int u = 0; u < U; ++u) load(kb + U + u, fb[u]);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < U; ++u) step(kb + u, fa[u]);
+#pragma unroll
+      for (int u = 0; u < U; ++u) step(kb + U + u, fb[u]);
+      kb += 2 * U;
+    } else {  // one batch left
+#pragma unroll
+      for (int u = 0; u < U; ++u) step(kb + u, fa[u]);
+      kb += U;
+    }
   }
   for (; kb < kb1; ++kb) {
-    v8i af[NT], bf[MT];
-    load(kb, af, bf);
-    step(kb, af, bf);
+    F f;
+    load(kb, f);
+    step(kb, f);
   }
 
-  // Cross-wave reduction: red[w][tile][i][lane].
+  // Cross-wave reduction over the KS waves of a group: red[wave][tile][i][lane].
   constexpr int TILES = NT * MT;
-  __shared__ float red[WAVES > 1 ? WAVES * TILES * 4 * 64 : 1];
-  if constexpr (WAVES > 1) {
+  __shared__ float red[KS > 1 ? 4 * TILES * 4 * 64 : 1];
+  if constexpr (KS > 1) {
 #pragma unroll
     for (int s = 0; s < NT; ++s)
 #pragma unroll
@@ -232,24 +309,27 @@ __global__ void __launch_bounds__(WAVES * 64) stream8_kernel(G8 p) {
         }
     __syncthreads();
   }
-  // Output subtile o = (so, t) finished by wave o % WAVES.
+  if (!has_cols) return;
+  // Output subtile o = (so, t) of the group is finished by its wave o % KS.
 #pragma unroll
   for (int so = 0; so < NTH; ++so)
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
       const int o = so * MT + t;
-      if (WAVES > 1 && (o % WAVES) != wave) continue;
+      if (KS > 1 && (o % KS) != ks) continue;
       float g[4], u[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        if constexpr (WAVES > 1) {
+        if constexpr (KS > 1) {
           float sg = 0.f, su = 0.f;
           int ig = 0, iu = 0;
-          for (int w = 0; w < WAVES; ++w) {
-            const float vg = red[((w * TILES + so * MT + t) * 4 + i) * 64 + lane];
+#pragma unroll
+          for (int w = 0; w < KS; ++w) {
+            const int src = ns * KS + w;
+            const float vg = red[((src * TILES + so * MT + t) * 4 + i) * 64 + lane];
             if (INT_ACC) ig += __float_as_int(vg); else sg += vg;
             if constexpr (EPI == kEpiGated) {
-              const float vu = red[((w * TILES + (so + NTH) * MT + t) * 4 + i) * 64 + lane];
+              const float vu = red[((src * TILES + (so + NTH) * MT + t) * 4 + i) * 64 + lane];
               if (INT_ACC) iu += __float_as_int(vu); else su += vu;
             }
           }
@@ -263,6 +343,206 @@ __global__ void __launch_bounds__(WAVES * 64) stream8_kernel(G8 p) {
       }
       finish4<KIND, EPI, ACT, MOE>(p, orow[t], brow[t], bval[t], nout0 + 16 * so + 4 * g4, g, u);
     }
+}
+
+// ============================================================ ring8
+// Decode-shaped GEMM through an LDS ring. A block is NW waves; wave w owns NT
+// 16-row weight subtiles and all NW waves share one 16-token subtile, over
+// the whole K. Each 128-K step is a ring slot filled by direct global->LDS
+// copies of whole 128-byte lines (8 operand rows x 128 B per copy: each
+// wave's weights, the shared token rows, one 4-byte-per-lane copy of the
+// step's scales), XOR-swizzled like the tiled kernel so the MFMA fragment
+// reads are conflict-free. R-1 slots are in flight while one is consumed and
+// in-flight data costs no registers. Whole-line copies stream from HBM
+// markedly faster than the 16-row x 64-byte pattern of register fragments.
+template <int KIND, int NT, bool MOE, int EPI, int ACT, int R, bool WX128, int TQ, int NW>
+__global__ void __launch_bounds__(64 * NW) ring8_kernel(G8 p) {
+  constexpr bool GATED = (EPI == kEpiGated);
+  constexpr int NTH = GATED ? NT / 2 : NT;
+  constexpr bool INT_ACC = (KIND == kI8Token);
+  constexpr bool SCALES = (KIND != kI8Token);
+  // TQ token copies of 8 rows per slot: 1 when the block has at most 8 token
+  // rows (lanes of the missing rows read row 0), else 2.
+  static_assert(TQ == 1 || TQ == 2, "one or two 8-row token copies");
+  static_assert(NW == 1 || KIND != kI8Group, "int8 group weight scales need one lane per weight row");
+  constexpr int WQ = 2 * NT;                        // weight copies per wave and slot
+  constexpr int EX = TQ + (SCALES ? 1 : 0);         // shared copies per slot
+  static_assert(NW == 1 || EX <= NW, "one shared copy per wave at most");
+  constexpr int E_HI = NW == 1 ? EX : 1;            // shared copies of a wave that has any
+  constexpr int TOK_OFF = NW * NT * 2048;
+  constexpr int SC_OFF = TOK_OFF + 2048;
+  constexpr int SLOT = SC_OFF + (SCALES ? 256 : 0);
+  static_assert((R - 2) * (WQ + E_HI) < 64, "vmcnt counts at most 63 copies");
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[R * SLOT];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = NW == 1 ? 0 : __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r16 = lane & 15, g4 = lane >> 4;
+  const int m0 = blockIdx.y * 16;
+  int expert = 0;
+  if constexpr (MOE) {
+    if (m0 >= *p.num_post) return;
+    expert = p.expert_ids[blockIdx.y];
+    if (expert < 0) return;
+  }
+  const int nout0 = (blockIdx.x * NW + wave) * (16 * NTH);
+  int wrow0[NT];
+#pragma unroll
+  for (int s = 0; s < NT; ++s) {
+    if constexpr (GATED)
+      wrow0[s] = s < NTH ? nout0 + 16 * s : p.gate_off + nout0 + 16 * (s - NTH);
+    else
+      wrow0[s] = nout0 + 16 * s;
+  }
+  const uint8_t* wbase = p.w + (int64_t)expert * p.w_es;
+
+  // Weight copy q of this wave moves its operand rows 8q..8q+7; lane l takes
+  // row 8q + l/8 and writes LDS position l%8 of that row with the row's chunk
+  // (l%8) ^ swz(row).
+  const int crow = lane >> 3;
+  const uint8_t* wsrc[WQ];
+#pragma unroll
+  for (int q = 0; q < WQ; ++q) {
+    const int row = 8 * q + crow;
+    const int wr = min(wrow0[row >> 4] + (row & 15), p.N - 1);
+    wsrc[q] = wbase + (int64_t)wr * p.ldw + 16 * ((lane & 7) ^ lds_swz(row & 15));
+  }
+  // Shared copy of this wave (NW > 1: wave e < EX issues shared copy e; NW == 1:
+  // the only wave issues all EX): e < TQ is token rows 8e..8e+7, e == TQ the scales.
+  const int e0 = NW == 1 ? 0 : wave;
+  const int ne = NW == 1 ? EX : (wave < EX ? 1 : 0);
+  const uint8_t* tsrc[TQ];
+#pragma unroll
+  for (int e = 0; e < TQ; ++e) {
+    const int row = 8 * e + crow;
+    int br, orw;
+    bool v;
+    token_row<MOE>(p, m0 + row, br, orw, v);
+    tsrc[e] = p.a + (int64_t)br * p.lda + 16 * ((lane & 7) ^ lds_swz(row));
+  }
+  // Scale copy: lanes 0..15 the token rows' activation scales, lanes 16.. the
+  // weight scales (fp8: one per subtile of the block; int8 group: one per row).
+  const float* ssrc = nullptr;
+  int64_t sstride = 0;
+  if constexpr (SCALES) {
+    int br, orw;
+    bool v;
+    if (lane < 16) {
+      token_row<MOE>(p, m0 + lane, br, orw, v);
+      ssrc = p.sa + (int64_t)br * p.sa_rs;
+      sstride = p.sa_ks;
+    } else {
+      const float* swb = p.sw + (int64_t)expert * p.sw_es;
+      int wr;
+      if constexpr (KIND == kFp8Block) {
+        const int j = min(lane - 16, NW * NT - 1);  // subtile j of the block
+        const int jw = j / NT, js = j % NT;           // its wave and slot
+        const int n0 = (blockIdx.x * NW + jw) * (16 * NTH);
+        const int r0 = GATED ? (js < NTH ? n0 + 16 * js : p.gate_off + n0 + 16 * (js - NTH)) : n0 + 16 * js;
+        wr = min(r0, p.N - 1) >> 7;
+      } else {
+        const int j = min(lane - 16, 16 * NT - 1);
+        wr = min(wrow0[j >> 4] + (j & 15), p.N - 1);
+      }
+      ssrc = swb + (int64_t)wr * p.sw_ns;
+      sstride = p.sw_ks;
+    }
+  }
+  auto issue = [&](int kb, int slot) {
+    uint8_t* st = ring + slot * SLOT;
+    const int64_t ko = (int64_t)kb * 128;
+#pragma unroll
+    for (int q = 0; q < WQ; ++q) g2l_b128(wsrc[q] + ko, st + wave * NT * 2048 + q * 1024);
+    for (int e = e0; e < e0 + ne; ++e) {
+      if (e < TQ) g2l_b128(tsrc[e] + ko, st + TOK_OFF + e * 1024);
+      else if constexpr (SCALES) g2l_b32(ssrc + (int64_t)kb * sstride, st + SC_OFF);
+    }
+  };
+
+  const uint32_t frag0 = (uint32_t)r16 * 128 + 16 * (g4 ^ lds_swz(r16));
+  const uint32_t frag1 = (uint32_t)r16 * 128 + 16 * ((4 + g4) ^ lds_swz(r16));
+  const int tr = (TQ == 1 && r16 >= 8) ? 0 : r16;  // token row this lane reads
+  const uint32_t tfrag0 = (uint32_t)tr * 128 + 16 * (g4 ^ lds_swz(tr));
+  const uint32_t tfrag1 = (uint32_t)tr * 128 + 16 * ((4 + g4) ^ lds_swz(tr));
+  v4f acc[NT];
+  v4i acci[NT];
+#pragma unroll
+  for (int s = 0; s < NT; ++s) {
+    acc[s] = v4f{0.f, 0.f, 0.f, 0.f};
+    acci[s] = v4i{0, 0, 0, 0};
+  }
+
+  const int nks = p.K >> 7;
+#pragma unroll
+  for (int s0 = 0; s0 < R - 1; ++s0)
+    if (s0 < nks) issue(s0, s0);
+  int slot = 0;
+  for (int kb = 0; kb < nks; ++kb) {
+    constexpr int AHEAD = R - 2;  // slots issued after slot kb, in steady state
+    if (kb + AHEAD <= nks - 1) {
+      if (ne == E_HI) wait_vmcnt<AHEAD * (WQ + E_HI)>(); else wait_vmcnt<AHEAD * WQ>();
+    } else {
+      wait_vmcnt<0>();
+    }
+    if constexpr (NW > 1) lds_barrier();  // shared token and scale copies of other waves
+    const uint8_t* st = ring + slot * SLOT;
+    const v8i bf = cat8(lds128(st + TOK_OFF + tfrag0), lds128(st + TOK_OFF + tfrag1));
+    v8i af[NT];
+#pragma unroll
+    for (int s = 0; s < NT; ++s) {
+      const uint8_t* sub = st + (wave * NT + s) * 2048;
+      af[s] = cat8(lds128(sub + frag0), lds128(sub + frag1));
+      if constexpr (WX128) af[s] = flip80(af[s]);
+    }
+    float sa = 0.f, sw[NT][4];
+    if constexpr (SCALES) {
+      const float* sl = reinterpret_cast<const float*>(st + SC_OFF);
+      sa = sl[r16];
+#pragma unroll
+      for (int s = 0; s < NT; ++s)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          sw[s][i] = KIND == kFp8Block ? sl[16 + wave * NT + s] : sl[16 + 16 * s + 4 * g4 + i];
+    }
+    // The slot consumed last step is free: every wave has passed this step's
+    // barrier, so its fragments are in registers.
+    const int next = kb + R - 1;
+    if (next < nks) issue(next, slot == 0 ? R - 1 : slot - 1);
+#pragma unroll
+    for (int s = 0; s < NT; ++s) {
+      if constexpr (KIND == kFp8Block) {
+        const v4f part = mfma_fp8(af[s], bf, v4f{0.f, 0.f, 0.f, 0.f});
+        const float c = sw[s][0] * sa;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[s][i] = fmaf(part[i], c, acc[s][i]);
+      } else if constexpr (KIND == kI8Token) {
+        acci[s] = mfma_i8(lo4(af[s]), lo4(bf), acci[s]);
+        acci[s] = mfma_i8(hi4(af[s]), hi4(bf), acci[s]);
+      } else {
+        v4i part = mfma_i8(lo4(af[s]), lo4(bf), v4i{0, 0, 0, 0});
+        part = mfma_i8(hi4(af[s]), hi4(bf), part);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[s][i] = fmaf((float)part[i], sw[s][i] * sa, acc[s][i]);
+      }
+    }
+    slot = slot == R - 1 ? 0 : slot + 1;
+  }
+
+  if (nout0 >= p.n_out) return;
+  int brow, orow;
+  bool bval;
+  token_row<MOE>(p, m0 + r16, brow, orow, bval);
+#pragma unroll
+  for (int so = 0; so < NTH; ++so) {
+    float g[4], u[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      g[i] = INT_ACC ? __int_as_float(acci[so][i]) : acc[so][i];
+      if constexpr (GATED) u[i] = INT_ACC ? __int_as_float(acci[so + NTH][i]) : acc[so + NTH][i];
+      else u[i] = 0.f;
+    }
+    finish4<KIND, EPI, ACT, MOE>(p, orow, brow, bval, nout0 + 16 * so + 4 * g4, g, u);
+  }
 }
 
 // ============================================================ tiled8
@@ -558,12 +838,38 @@ __global__ void __launch_bounds__(WM * WN * 64) tiled8_kernel(G8 p, int tiles_m,
 }
 
 // ============================================================ launchers
-template <int KIND, int NT, int MT, int WAVES, bool MOE, int EPI, int ACT, int U, bool WX128>
+// Token rows go to LDS when one 16-row subtile of them fits next to a second
+// block on the CU (16 x K bytes <= 80 KiB); otherwise they stream with the weights.
+constexpr int64_t kTokLdsMax = 80 * 1024;
+
+template <int KIND, int NT, int MT, int KS, bool MOE, int EPI, int ACT, int U, bool WX128>
 int launch_stream(const G8& p, int grid_y, hipStream_t st, const char* op) {
   constexpr int NTH = (EPI == kEpiGated) ? NT / 2 : NT;
-  const int grid_x = (p.n_out + 16 * NTH - 1) / (16 * NTH);
-  hipLaunchKernelGGL((stream8_kernel<KIND, NT, MT, WAVES, MOE, EPI, ACT, U, WX128>), dim3(grid_x, grid_y),
-                     dim3(WAVES * 64), 0, st, p);
+  constexpr int NS = 4 / KS;
+  const int groups = (p.n_out + 16 * NTH - 1) / (16 * NTH);
+  const int grid_x = (groups + NS - 1) / NS;
+  const int64_t tok_bytes = 16 * (int64_t)p.K;
+  if (MT == 1 && tok_bytes <= kTokLdsMax) {
+    hipLaunchKernelGGL((stream8_kernel<KIND, NT, MT, KS, MOE, EPI, ACT, U, WX128, MT == 1>), dim3(grid_x, grid_y),
+                       dim3(256), (size_t)tok_bytes, st, p);
+  } else {
+    hipLaunchKernelGGL((stream8_kernel<KIND, NT, MT, KS, MOE, EPI, ACT, U, WX128, false>), dim3(grid_x, grid_y),
+                       dim3(256), 0, st, p);
+  }
+  return check_launch(op);
+}
+
+template <int KIND, int NT, bool MOE, int EPI, int ACT, int R, bool WX128, int NW>
+int launch_ring(const G8& p, int grid_y, hipStream_t st, const char* op) {
+  constexpr int NTH = (EPI == kEpiGated) ? NT / 2 : NT;
+  const int groups = (p.n_out + 16 * NTH - 1) / (16 * NTH);
+  const int grid_x = (groups + NW - 1) / NW;
+  if (!MOE && p.M <= 8)
+    hipLaunchKernelGGL((ring8_kernel<KIND, NT, MOE, EPI, ACT, R, WX128, 1, NW>), dim3(grid_x, grid_y), dim3(64 * NW),
+                       0, st, p);
+  else
+    hipLaunchKernelGGL((ring8_kernel<KIND, NT, MOE, EPI, ACT, R, WX128, 2, NW>), dim3(grid_x, grid_y), dim3(64 * NW),
+                       0, st, p);
   return check_launch(op);
 }
 
@@ -624,15 +930,14 @@ template <int KIND, int EPI, bool WX128>
 int dense_dispatch(const G8& p, hipStream_t st, const char* op, int cfg) {
   const int M = p.M;
   if (cfg < 0) {
-    if (M <= 16) cfg = 0;
-    else if (M <= 32) cfg = 1;
+    if (M <= 32) cfg = 0;
     else if (M <= 64) cfg = 2;
     else if (M <= 512) cfg = 3;
     else cfg = 5;
   }
   switch (cfg) {
-    case 0: return launch_stream<KIND, 1, 1, 8, false, EPI, kActSilu, 4, WX128>(p, (M + 15) / 16, st, op);
-    case 1: return launch_stream<KIND, 1, 2, 8, false, EPI, kActSilu, 4, WX128>(p, (M + 31) / 32, st, op);
+    case 0: return launch_ring<KIND, 1, false, EPI, kActSilu, 5, WX128, 1>(p, (M + 15) / 16, st, op);
+    case 1: return launch_stream<KIND, 1, 2, 4, false, EPI, kActSilu, 4, WX128>(p, (M + 31) / 32, st, op);
     case 2: return launch_stream<KIND, 1, 4, 4, false, EPI, kActSilu, 2, WX128>(p, (M + 63) / 64, st, op);
     case 3: return launch_tiled<KIND, 128, 128, 2, 2, 4, false, EPI, kActSilu, WX128>(p, 0, st, op);
     case 4: return launch_tiled<KIND, 256, 64, 4, 2, 3, false, EPI, kActSilu, WX128>(p, 0, st, op);
@@ -641,7 +946,13 @@ int dense_dispatch(const G8& p, hipStream_t st, const char* op, int cfg) {
       // int8 group scales need one copy per 64 weight rows: 4 waves cannot carry 256 rows of them.
       if constexpr (KIND == kI8Group) return launch_tiled<KIND, 128, 128, 2, 2, 4, false, EPI, kActSilu, WX128>(p, 0, st, op);
       else return launch_tiled<KIND, 128, 256, 2, 2, 3, false, EPI, kActSilu, WX128>(p, 0, st, op);
-    default: return set_error(STRIX_ERR_INVALID, "%s: cfg must be in 0..6, got %d", op, cfg);
+    // Decode sweep points (token rows per wave, waves splitting K, K-steps per batch).
+    case 7: return launch_stream<KIND, 1, 1, 2, false, EPI, kActSilu, 4, WX128>(p, (M + 15) / 16, st, op);
+    case 8: return launch_stream<KIND, 1, 1, 4, false, EPI, kActSilu, 4, WX128>(p, (M + 15) / 16, st, op);
+    case 9: return launch_ring<KIND, 1, false, EPI, kActSilu, 7, WX128, KIND == kI8Group ? 1 : 4>(p, (M + 15) / 16, st, op);
+    case 10: return launch_ring<KIND, 1, false, EPI, kActSilu, 7, WX128, 1>(p, (M + 15) / 16, st, op);
+    case 11: return launch_ring<KIND, 1, false, EPI, kActSilu, 6, WX128, KIND == kI8Group ? 1 : 4>(p, (M + 15) / 16, st, op);
+    default: return set_error(STRIX_ERR_INVALID, "%s: cfg must be in 0..11, got %d", op, cfg);
   }
 }
 
@@ -650,8 +961,8 @@ template <int KIND, int EPI, int ACT>
 int moe_dispatch(const G8& p, int block_m, int num_blocks, hipStream_t st, const char* op) {
   constexpr int NTS = (EPI == kEpiGated) ? 2 : 1;
   switch (block_m) {
-    case 16: return launch_stream<KIND, NTS, 1, 4, true, EPI, ACT, 2, false>(p, num_blocks, st, op);
-    case 32: return launch_stream<KIND, NTS, 2, 4, true, EPI, ACT, 2, false>(p, num_blocks, st, op);
+    case 16: return launch_ring<KIND, NTS, true, EPI, ACT, 5, false, 1>(p, num_blocks, st, op);
+    case 32: return launch_stream<KIND, NTS, 2, 2, true, EPI, ACT, 4, false>(p, num_blocks, st, op);
     case 64: return launch_tiled<KIND, 64, 128, 1, 4, 4, true, EPI, ACT, false>(p, num_blocks, st, op);
     case 128: return launch_tiled<KIND, 128, 128, 2, 2, 4, true, EPI, ACT, false>(p, num_blocks, st, op);
     case 256: return launch_tiled<KIND, 256, 128, 4, 2, 3, true, EPI, ACT, false>(p, num_blocks, st, op);

@@ -46,7 +46,7 @@ def test_shapes_and_ragged_n(m, n, k):
     assert peak_rel_err(out, oracle.fp8_block_gemm(qa, sa, d["w"], d["sw"])) <= TOL
 
 
-@pytest.mark.parametrize("cfg", range(7))
+@pytest.mark.parametrize("cfg", range(12))
 def test_every_cfg(cfg):
     d = workloads.c2_fp8(seed=cfg, m=70, n=640, k=1536)
     qa, sa = oracle.fp8_quant_group128(d["x"])
