@@ -84,6 +84,35 @@ __device__ __forceinline__ float wscale(const G16& p, int e, int n, int k) {
   }
 }
 
+// Split form of wscale/wzero for prefetching: the raw bits are loaded with
+// the weights and turned into values when the weights are decoded.
+__device__ __forceinline__ int64_t wscale_row(const G16& p, int e, int n) {
+  return (int64_t)e * p.ws_es + (int64_t)(n / p.ws_nblock) * p.ws_ns;
+}
+__device__ __forceinline__ uint32_t wscale_raw(const G16& p, int64_t row_idx, int k) {
+  const int64_t idx = row_idx + (p.ws_kgroup ? (int64_t)(k / p.ws_kgroup) * p.ws_ks : 0);
+  switch (p.ws_kind) {
+    case kSF32: return static_cast<const uint32_t*>(p.ws)[idx];
+    case kSBf16:
+    case kSF16: return static_cast<const uint16_t*>(p.ws)[idx];
+    default: return static_cast<const uint8_t*>(p.ws)[idx];
+  }
+}
+__device__ __forceinline__ float wscale_value(const G16& p, uint32_t raw) {
+  switch (p.ws_kind) {
+    case kSF32: return __uint_as_float(raw);
+    case kSBf16: return bf16_bits_to_f32(raw);
+    case kSF16: return f16_bits_to_f32(raw);
+    default: return __uint_as_float(raw << 23);  // 2^(b-127); b == 0 gives +0: the zero block
+  }
+}
+__device__ __forceinline__ int64_t wzero_row(const G16& p, int e, int n) {
+  return (int64_t)e * p.wz_es + (int64_t)(n >> 1) * p.wz_ns;
+}
+__device__ __forceinline__ uint32_t wzero_raw(const G16& p, int64_t row_idx, int k) {
+  return p.wz[row_idx + (int64_t)(k / p.ws_kgroup) * p.wz_ks];
+}
+
 __device__ __forceinline__ float wzero(const G16& p, int e, int n, int k) {
   const uint32_t b = p.wz[(int64_t)e * p.wz_es + (int64_t)(n >> 1) * p.wz_ns + (int64_t)(k / p.ws_kgroup) * p.wz_ks];
   return (float)((n & 1) ? (b >> 4) : (b & 15));
@@ -100,6 +129,50 @@ __device__ __forceinline__ float e2m1_mag(uint32_t c) {
   const uint32_t e = c >> 1, m = c & 1;
   const uint32_t bits = e ? (((e + 126u) << 23) | (m << 22)) : (m ? 0x3f000000u : 0u);
   return __uint_as_float(bits);
+}
+
+// MXFP4 -> bf16 by table. With an e8m0 scale 2^(b-127) every decoded value
+// is exact in bf16, and for 2 <= b <= 252 it stays a normal number, so its
+// bits are the unit-scale bits of the magnitude plus (b-127) in the exponent
+// field. The 8-entry table of scaled magnitudes is split into a low-byte and
+// a high-byte table of 8 bytes each, which v_perm_b32 indexes with four
+// 3-bit magnitude codes at a time; the sign bit goes into the high byte. An
+// e8m0 of 0 is the zero block (signed zeros, like value * 0). Other exponents
+// take the scalar path.
+struct Mxfp4Lut {
+  uint32_t lo_l, lo_h, hi_l, hi_h;  // bytes of the table entries 0..3 / 4..7
+};
+__device__ __forceinline__ bool mxfp4_lut_ok(uint32_t b) { return b == 0u || (b >= 2u && b <= 252u); }
+__device__ __forceinline__ Mxfp4Lut mxfp4_lut(uint32_t b) {
+  // Unit-scale bf16 bits of the magnitudes 0, .5, 1, 1.5, 2, 3, 4, 6.
+  const int dlt = ((int)b - 127) << 7;
+  auto e = [&](int base) -> uint32_t { return b == 0u ? 0u : (uint32_t)(base + dlt); };
+  const uint32_t t01 = e(0x3F00) << 16;
+  const uint32_t t23 = e(0x3F80) | (e(0x3FC0) << 16);
+  const uint32_t t45 = e(0x4000) | (e(0x4040) << 16);
+  const uint32_t t67 = e(0x4080) | (e(0x40C0) << 16);
+  Mxfp4Lut t;
+  t.lo_l = __builtin_amdgcn_perm(t23, t01, 0x06040200u);
+  t.lo_h = __builtin_amdgcn_perm(t67, t45, 0x06040200u);
+  t.hi_l = __builtin_amdgcn_perm(t23, t01, 0x07050301u);
+  t.hi_h = __builtin_amdgcn_perm(t67, t45, 0x07050301u);
+  return t;
+}
+// 8 e2m1 codes of d (nibble i = value i) -> 4 dwords of bf16 pairs.
+__device__ __forceinline__ void mxfp4_dword_lut(uint32_t d, const Mxfp4Lut& t, uint32_t* out) {
+  const uint32_t me = d & 0x07070707u, mo = (d >> 4) & 0x07070707u;  // magnitudes of even / odd values
+  const uint32_t lo_e = __builtin_amdgcn_perm(t.lo_h, t.lo_l, me);
+  const uint32_t hi_e = __builtin_amdgcn_perm(t.hi_h, t.hi_l, me) | ((d << 4) & 0x80808080u);
+  const uint32_t lo_o = __builtin_amdgcn_perm(t.lo_h, t.lo_l, mo);
+  const uint32_t hi_o = __builtin_amdgcn_perm(t.hi_h, t.hi_l, mo) | (d & 0x80808080u);
+  const uint32_t e01 = __builtin_amdgcn_perm(hi_e, lo_e, 0x05010400u);  // values 0, 2
+  const uint32_t e23 = __builtin_amdgcn_perm(hi_e, lo_e, 0x07030602u);  // values 4, 6
+  const uint32_t o01 = __builtin_amdgcn_perm(hi_o, lo_o, 0x05010400u);  // values 1, 3
+  const uint32_t o23 = __builtin_amdgcn_perm(hi_o, lo_o, 0x07030602u);  // values 5, 7
+  out[0] = __builtin_amdgcn_perm(o01, e01, 0x05040100u);
+  out[1] = __builtin_amdgcn_perm(o01, e01, 0x07060302u);
+  out[2] = __builtin_amdgcn_perm(o23, e23, 0x05040100u);
+  out[3] = __builtin_amdgcn_perm(o23, e23, 0x07060302u);
 }
 
 // Decodes one dword of packed weights (8 values for 4-bit formats, 4 for
@@ -125,9 +198,9 @@ __device__ __forceinline__ void decode_dword(uint32_t d, float s, float z, uint3
       out[j] = pack2<F16>((q0 - z) * s, (q1 - z) * s);
     }
   } else if constexpr (FMT == kWFp8) {
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-      out[j] = pack2<F16>(e4m3_to_f32((d >> (16 * j)) & 0xffu) * s, e4m3_to_f32((d >> (16 * j + 8)) & 0xffu) * s);
+    const f32x2_t v01 = e4m3x2_to_f32<false>(d), v23 = e4m3x2_to_f32<true>(d);
+    out[0] = pack2<F16>(v01[0] * s, v01[1] * s);
+    out[1] = pack2<F16>(v23[0] * s, v23[1] * s);
   } else if constexpr (FMT == kWInt8) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -292,11 +365,23 @@ __global__ void __launch_bounds__(WAVES * 64) stream16_kernel(G16 p) {
 // ============================================================ tiled16
 // One 64-K stage per LDS buffer: weight rows 0..BN-1 (decoded by the block's
 // threads), token rows BN..BN+BM-1 (direct copies), 128 bytes per row,
-// swizzled. Three buffers: while stage kb is computed, stage kb+1 is decoded
-// and stage kb+2 is in flight.
-template <int FMT, int BM, int BN, int WM, int WN, bool MOE, int EPI, int ACT, bool F16>
-__global__ void __launch_bounds__(WM * WN * 64) tiled16_kernel(G16 p, int tiles_m, int tiles_n, int group_m) {
-  constexpr int W = WM * WN, T = W * 64;
+// swizzled. Three buffers and a two-deep register pipeline of raw weights:
+// while stage kb is computed, stage kb+1 is decoded into LDS from registers
+// loaded two steps earlier, the token rows of stage kb+2 are in flight, and
+// the raw weights of stage kb+3 are being fetched. Every load is issued
+// unconditionally (indices past the end are clamped, their buffers never
+// read), so each wait counts exactly the loads of later stages.
+//
+// NP > 0 specializes the waves: WM x WN consumer waves only run the MFMAs
+// of stage kb while NP producer waves issue every load and decode stage
+// kb+1 into LDS, so with one wave of each kind per SIMD the decode ALU work
+// runs under the MFMAs instead of in turn with them. NP == 0: every wave
+// decodes its share, then computes.
+template <int FMT, int BM, int BN, int WM, int WN, int NP, bool MOE, int EPI, int ACT, bool F16>
+__global__ void __launch_bounds__((WM * WN + NP) * 64) tiled16_kernel(G16 p, int tiles_m, int tiles_n, int group_m) {
+  constexpr int W = WM * WN;                 // MFMA waves
+  constexpr int PW = NP > 0 ? NP : W;        // waves that load and decode
+  constexpr int T = PW * 64;                 // their threads
   constexpr int TM = BM / WM, TN = BN / WN;
   constexpr int MT = TM / 16, NT = TN / 16;
   constexpr int SA = BN / 16;
@@ -310,8 +395,8 @@ __global__ void __launch_bounds__(WM * WN * 64) tiled16_kernel(G16 p, int tiles_
   constexpr int PPT = DIRECT_W ? 0 : (PIECES + T - 1) / T;  // pieces per thread (the last round may be partial)
   constexpr int ACOPY = BM / 8;                  // token row copies (8 rows each)
   constexpr int WCOPY = DIRECT_W ? BN / 8 : 0;
-  static_assert((ACOPY + WCOPY) % W == 0, "copies split evenly over the waves");
-  constexpr int CPW = (ACOPY + WCOPY) / W;
+  static_assert((ACOPY + WCOPY) % PW == 0, "copies split evenly over the loading waves");
+  constexpr int CPW = (ACOPY + WCOPY) / PW;
   constexpr bool GATED = (EPI == kEpiGated);
   constexpr int NTH = GATED ? NT / 2 : NT;
   static_assert(!GATED || NT % 2 == 0, "gated wave tiles pair gate and up subtiles");
@@ -321,7 +406,14 @@ __global__ void __launch_bounds__(WM * WN * 64) tiled16_kernel(G16 p, int tiles_
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r16 = lane & 15, g4 = lane >> 4;
-  const int wm = wave % WM, wn = wave / WM;
+  const bool is_prod = NP == 0 || wave >= W;
+  const bool is_cons = NP == 0 || wave < W;
+  // Index among the loading waves. MFMA waves never load; their (unused)
+  // copy and piece slots are computed as loading wave 0's so that every
+  // address formed in the set-up below stays in range.
+  const int pwave = NP > 0 ? max(wave - W, 0) : wave;
+  const int ptid = NP > 0 ? max(tid - W * 64, 0) : tid;
+  const int wm = wave % WM, wn = (wave / WM) % WN;
   int tm, tn, expert = 0;
   if constexpr (MOE) {
     tn = blockIdx.x;
@@ -348,7 +440,7 @@ __global__ void __launch_bounds__(WM * WN * 64) tiled16_kernel(G16 p, int tiles_
   bool qis_w[CPW > 0 ? CPW : 1];
 #pragma unroll
   for (int j = 0; j < CPW; ++j) {
-    const int q = wave + W * j;
+    const int q = pwave + PW * j;
     const int row = 8 * q + (lane >> 3);  // LDS row: weights first when copied directly
     if (DIRECT_W && row < BN) {
       const int r = min(wrow_of(row), p.N - 1);
@@ -368,38 +460,64 @@ __global__ void __launch_bounds__(WM * WN * 64) tiled16_kernel(G16 p, int tiles_
   int prow[PPT > 0 ? PPT : 1], pidx[PPT > 0 ? PPT : 1], pgrow[PPT > 0 ? PPT : 1];
 #pragma unroll
   for (int j = 0; j < PPT; ++j) {
-    const int pi = min(tid + T * j, PIECES - 1);  // surplus threads repeat the last piece (same bytes, same slot)
+    const int pi = min(ptid + T * j, PIECES - 1);  // surplus threads repeat the last piece (same bytes, same slot)
     prow[j] = pi / PPR;
     pidx[j] = pi % PPR;
     pgrow[j] = min(wrow_of(prow[j]), p.N - 1);
   }
-  u32x4 wraw[PPT > 0 ? PPT : 1];
-
-  auto load_w = [&](int kb) {
+  constexpr int PB = PPT > 0 ? PPT : 1;
+  constexpr bool ZP = (FMT == kWInt4Zp);
+  // Raw weights of one stage with their scale bits (and zero-point bytes).
+  struct WBuf {
+    u32x4 w[PB];
+    uint32_t s[PB];
+    uint32_t z[PB];
+  };
+  int64_t srow[PB], zrow[PB];
 #pragma unroll
-    for (int j = 0; j < PPT; ++j)
-      wraw[j] = ldg128(wbase + (int64_t)pgrow[j] * p.ldw + (int64_t)(kb * 64 + pidx[j] * PV) * BITS / 8);
+  for (int j = 0; j < PPT; ++j) {
+    srow[j] = wscale_row(p, expert, pgrow[j]);
+    zrow[j] = ZP ? wzero_row(p, expert, pgrow[j]) : 0;
+  }
+  auto load_w = [&](int kb, WBuf& b) {
+#pragma unroll
+    for (int j = 0; j < PPT; ++j) {
+      const int k = kb * 64 + pidx[j] * PV;
+      b.w[j] = ldg128(wbase + (int64_t)pgrow[j] * p.ldw + (int64_t)k * BITS / 8);
+      if constexpr (!DIRECT_W) b.s[j] = wscale_raw(p, srow[j], k);
+      if constexpr (ZP) b.z[j] = wzero_raw(p, zrow[j], k);
+    }
   };
   auto copy_a = [&](int kb, int buf) {
     uint8_t* st = smem + buf * STAGE;
 #pragma unroll
     for (int j = 0; j < CPW; ++j) {
-      const int q = wave + W * j;
+      const int q = pwave + PW * j;
       const uint8_t* base = qis_w[j] ? wbase + (int64_t)kb * 128 : reinterpret_cast<const uint8_t*>(p.a) + (int64_t)kb * 128;
       g2l_b128(base + qoff[j], st + (DIRECT_W ? q : q + BN / 8) * 1024);
     }
   };
-  auto decode_w = [&](int kb, int buf) {
+  auto decode_w = [&](int buf, const WBuf& b) {
     uint8_t* st = smem + buf * STAGE;
 #pragma unroll
     for (int j = 0; j < PPT; ++j) {
-      const int k = kb * 64 + pidx[j] * PV;
-      const float sc = wscale(p, expert, pgrow[j], k);
-      const float z = (FMT == kWInt4Zp) ? wzero(p, expert, pgrow[j], k) : 8.0f;
+      const float sc = wscale_value(p, b.s[j]);
+      const float z = ZP ? (float)((pgrow[j] & 1) ? (b.z[j] >> 4) : (b.z[j] & 15)) : 8.0f;
       uint32_t v[PV / 2];
       constexpr int PAIRS_PER_DWORD = 32 / BITS / 2;
+      if constexpr (FMT == kWMxfp4 && !F16) {
+        if (p.ws_kind == kSE8m0 && mxfp4_lut_ok(b.s[j])) {
+          const Mxfp4Lut t = mxfp4_lut(b.s[j]);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) decode_dword<FMT, F16>(wraw[j][i], sc, z, &v[i * PAIRS_PER_DWORD]);
+          for (int i = 0; i < 4; ++i) mxfp4_dword_lut(b.w[j][i], t, &v[4 * i]);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) decode_dword<FMT, F16>(b.w[j][i], sc, z, &v[i * PAIRS_PER_DWORD]);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) decode_dword<FMT, F16>(b.w[j][i], sc, z, &v[i * PAIRS_PER_DWORD]);
+      }
       const int row = prow[j];
 #pragma unroll
       for (int c = 0; c < PV / 8; ++c) {
@@ -427,22 +545,8 @@ __global__ void __launch_bounds__(WM * WN * 64) tiled16_kernel(G16 p, int tiles_
     for (int t = 0; t < MT; ++t) acc[s][t] = v4f{0.f, 0.f, 0.f, 0.f};
 
   const int nkb = p.K >> 6;
-  load_w(0);
-  copy_a(0, 0);
-  wait_vmcnt<0>();
-  decode_w(0, 0);
-  if (nkb > 1) {
-    load_w(1);
-    copy_a(1, 1);
-  }
-  for (int kb = 0; kb < nkb; ++kb) {
-    wait_vmcnt<0>();
-    if (kb + 1 < nkb) decode_w(kb + 1, (kb + 1) % STAGES);
-    lds_barrier();
-    if (kb + 2 < nkb) {
-      load_w(kb + 2);
-      copy_a(kb + 2, (kb + 2) % STAGES);
-    }
+  auto clampk = [&](int kb) { return kb < nkb ? kb : nkb - 1; };
+  auto compute = [&](int kb) {
     const uint8_t* st = smem + (kb % STAGES) * STAGE;
 #pragma unroll
     for (int step = 0; step < 2; ++step) {
@@ -462,7 +566,42 @@ __global__ void __launch_bounds__(WM * WN * 64) tiled16_kernel(G16 p, int tiles_
         }
       }
     }
+  };
+  // Iteration kb: copies of stage kb were issued at kb-2, followed by the raw
+  // weights (and scale, zero-point loads) of kb+2 and the copies of kb+1.
+  constexpr int LPW = DIRECT_W ? 0 : PPT * (2 + (ZP ? 1 : 0));  // loads per stage of load_w
+  auto body = [&](int kb, WBuf& wdec) {
+    if (is_prod) {
+      wait_vmcnt<LPW + CPW>();
+      if constexpr (NP == 0) decode_w((kb + 1) % STAGES, wdec);
+    }
+    lds_barrier();
+    if (is_prod) {
+      if constexpr (NP > 0) decode_w((kb + 1) % STAGES, wdec);
+      load_w(clampk(kb + 3), wdec);
+      copy_a(clampk(kb + 2), (kb + 2) % STAGES);
+    }
+    if (is_cons) compute(kb);
+  };
+  WBuf wA, wB;  // raw weights of even / odd stages
+  if (is_prod) {
+    load_w(0, wA);
+    copy_a(0, 0);
+    wait_vmcnt<0>();
+    decode_w(0, wA);
+    load_w(clampk(1), wB);
+    copy_a(clampk(1), 1);
+    load_w(clampk(2), wA);
   }
+  int kb = 0;
+  for (; kb + 1 < nkb; kb += 2) {
+    body(kb, wB);
+    body(kb + 1, wA);
+  }
+  if (kb < nkb) body(kb, wB);
+  // Copies of clamped stages may still be landing: none may outlive the block.
+  wait_vmem();
+  if (!is_cons) return;
 
 #pragma unroll
   for (int t = 0; t < MT; ++t) {
@@ -510,8 +649,20 @@ __global__ void __launch_bounds__(256) dequant_kernel(G16 p, uint16_t* out, int6
   const float z = (FMT == kWInt4Zp) ? wzero(p, 0, n, k) : 8.0f;
   uint32_t v[PV / 2];
   constexpr int PAIRS_PER_DWORD = 32 / BITS / 2;
+  bool done = false;
+  if constexpr (FMT == kWMxfp4) {
+    const uint32_t b = p.ws_kind == kSE8m0 ? wscale_raw(p, wscale_row(p, 0, n), k) : 1u;
+    if (p.ws_kind == kSE8m0 && mxfp4_lut_ok(b)) {
+      const Mxfp4Lut t = mxfp4_lut(b);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) decode_dword<FMT, false>(raw[j], sc, z, &v[j * PAIRS_PER_DWORD]);
+      for (int j = 0; j < 4; ++j) mxfp4_dword_lut(raw[j], t, &v[4 * j]);
+      done = true;
+    }
+  }
+  if (!done) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) decode_dword<FMT, false>(raw[j], sc, z, &v[j * PAIRS_PER_DWORD]);
+  }
   uint16_t* o = out + (int64_t)n * ldo + k;
 #pragma unroll
   for (int c = 0; c < PV / 8; ++c) {
@@ -531,17 +682,18 @@ int launch_stream16(const G16& p, int grid_y, hipStream_t st, const char* op) {
   return check_launch(op);
 }
 
-template <int FMT, int BM, int BN, int WM, int WN, bool MOE, int EPI, int ACT, bool F16>
+template <int FMT, int BM, int BN, int WM, int WN, int NP, bool MOE, int EPI, int ACT, bool F16>
 int launch_tiled16(const G16& p, int grid_y_moe, hipStream_t st, const char* op) {
   constexpr int COLS = (EPI == kEpiGated) ? BN / 2 : BN;
+  constexpr int THREADS = (WM * WN + NP) * 64;
   const int tiles_n = (p.n_out + COLS - 1) / COLS;
   if constexpr (MOE) {
-    hipLaunchKernelGGL((tiled16_kernel<FMT, BM, BN, WM, WN, MOE, EPI, ACT, F16>), dim3(tiles_n, grid_y_moe),
-                       dim3(WM * WN * 64), 0, st, p, 0, tiles_n, 0);
+    hipLaunchKernelGGL((tiled16_kernel<FMT, BM, BN, WM, WN, NP, MOE, EPI, ACT, F16>), dim3(tiles_n, grid_y_moe),
+                       dim3(THREADS), 0, st, p, 0, tiles_n, 0);
   } else {
     const int tiles_m = (p.M + BM - 1) / BM;
-    hipLaunchKernelGGL((tiled16_kernel<FMT, BM, BN, WM, WN, MOE, EPI, ACT, F16>), dim3(tiles_m * tiles_n),
-                       dim3(WM * WN * 64), 0, st, p, tiles_m, tiles_n, 8);
+    hipLaunchKernelGGL((tiled16_kernel<FMT, BM, BN, WM, WN, NP, MOE, EPI, ACT, F16>), dim3(tiles_m * tiles_n),
+                       dim3(THREADS), 0, st, p, tiles_m, tiles_n, 8);
   }
   return check_launch(op);
 }
@@ -552,9 +704,9 @@ int moe16_dispatch(const G16& p, int block_m, int num_blocks, hipStream_t st, co
   switch (block_m) {
     case 16: return launch_stream16<FMT, NTS, 1, 4, true, EPI, ACT, F16>(p, num_blocks, st, op);
     case 32: return launch_stream16<FMT, NTS, 2, 4, true, EPI, ACT, F16>(p, num_blocks, st, op);
-    case 64: return launch_tiled16<FMT, 64, 128, 1, 4, true, EPI, ACT, F16>(p, num_blocks, st, op);
-    case 128: return launch_tiled16<FMT, 128, 128, 2, 2, true, EPI, ACT, F16>(p, num_blocks, st, op);
-    case 256: return launch_tiled16<FMT, 256, 128, 4, 2, true, EPI, ACT, F16>(p, num_blocks, st, op);
+    case 64: return launch_tiled16<FMT, 64, 256, 1, 4, 4, true, EPI, ACT, F16>(p, num_blocks, st, op);
+    case 128: return launch_tiled16<FMT, 128, 256, 2, 2, 4, true, EPI, ACT, F16>(p, num_blocks, st, op);
+    case 256: return launch_tiled16<FMT, 256, 128, 2, 2, 4, true, EPI, ACT, F16>(p, num_blocks, st, op);
     default: return set_error(STRIX_ERR_INVALID, "%s: block_m must be 16, 32, 64, 128 or 256, got %d", op, block_m);
   }
 }
@@ -567,10 +719,13 @@ int dense16_dispatch(const G16& p, hipStream_t st, const char* op, int cfg) {
     case 0: return launch_stream16<FMT, 1, 1, 8, false, kEpiStore, kActSilu, F16>(p, (M + 15) / 16, st, op);
     case 1: return launch_stream16<FMT, 1, 2, 8, false, kEpiStore, kActSilu, F16>(p, (M + 31) / 32, st, op);
     case 2: return launch_stream16<FMT, 1, 4, 4, false, kEpiStore, kActSilu, F16>(p, (M + 63) / 64, st, op);
-    case 3: return launch_tiled16<FMT, 128, 128, 2, 2, false, kEpiStore, kActSilu, F16>(p, 0, st, op);
-    case 4: return launch_tiled16<FMT, 256, 128, 4, 2, false, kEpiStore, kActSilu, F16>(p, 0, st, op);
-    case 5: return launch_tiled16<FMT, 64, 128, 1, 4, false, kEpiStore, kActSilu, F16>(p, 0, st, op);
-    default: return set_error(STRIX_ERR_INVALID, "%s: cfg must be in 0..5, got %d", op, cfg);
+    case 3: return launch_tiled16<FMT, 128, 256, 2, 2, 4, false, kEpiStore, kActSilu, F16>(p, 0, st, op);
+    case 4: return launch_tiled16<FMT, 256, 128, 2, 2, 4, false, kEpiStore, kActSilu, F16>(p, 0, st, op);
+    case 5: return launch_tiled16<FMT, 64, 256, 1, 4, 4, false, kEpiStore, kActSilu, F16>(p, 0, st, op);
+    // Sweep points: every wave decodes and computes.
+    case 6: return launch_tiled16<FMT, 128, 256, 2, 4, 0, false, kEpiStore, kActSilu, F16>(p, 0, st, op);
+    case 7: return launch_tiled16<FMT, 128, 128, 2, 2, 0, false, kEpiStore, kActSilu, F16>(p, 0, st, op);
+    default: return set_error(STRIX_ERR_INVALID, "%s: cfg must be in 0..7, got %d", op, cfg);
   }
 }
 

@@ -46,12 +46,12 @@ __device__ __forceinline__ void wait_vmcnt() {
 template <bool MOE, class P>
 __device__ __forceinline__ void token_row(const P& p, int m, int& brow, int& orow, bool& valid) {
   if constexpr (MOE) {
-    const int sid = (m < p.sorted_len) ? p.sorted_ids[m] : p.num_slots;
+    const int sid = (m >= 0 && m < p.sorted_len) ? p.sorted_ids[m] : p.num_slots;
     valid = sid >= 0 && sid < p.num_slots;
     brow = valid ? sid / p.top_k : 0;
     orow = sid;
   } else {
-    valid = m < p.M;
+    valid = m >= 0 && m < p.M;
     brow = valid ? m : 0;
     orow = m;
   }

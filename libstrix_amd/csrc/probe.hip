@@ -120,8 +120,6 @@ int strix_probe_g2l(const uint8_t* src, uint8_t* dst, void* stream) {
 // format definitions by tests (they decide which decoders the GEMMs may use).
 namespace strix {
 namespace {
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
 
 // out[s][b][j] (bf16 bits), j = 0,1: v_cvt_scalef32_pk_bf16_fp4 of byte b
 // (placed in byte lane `sel` of the source dword) with scale scales[s].

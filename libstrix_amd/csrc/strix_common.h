@@ -63,15 +63,15 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as
 __device__ __forceinline__ float bf16_lo(uint32_t p) { return __uint_as_float(p << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t p) { return __uint_as_float(p & 0xffff0000u); }
 
-// fp32 -> bf16 bits, round to nearest even (NaN stays NaN).
+// fp32 -> bf16 bits, round to nearest even: gfx950's v_cvt_pk_bf16_f32
+// (pinned equal to torch's cast by the converter probe test).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float x) {
-  uint32_t a = __float_as_uint(x);
-  if ((a & 0x7fffffffu) > 0x7f800000u) return (a >> 16) | 0x40u;
-  a += 0x7fffu + ((a >> 16) & 1u);
-  return a >> 16;
+  return __builtin_bit_cast(uint16_t, (__bf16)x);
 }
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+  const bf16x2_t r = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, r);
 }
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
@@ -90,6 +90,14 @@ template <bool IS_F16>
 __device__ __forceinline__ uint32_t f32_to_act_bits(float x) {
   if constexpr (IS_F16) return f32_to_f16_bits(x);
   else return f32_to_bf16_bits(x);
+}
+
+// Two e4m3fn bytes (bytes 0,1 of d when WORD_HI is false, else 2,3) -> fp32
+// with gfx950's v_cvt_pk_f32_fp8 (pinned against every code by the probe test).
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+template <bool WORD_HI>
+__device__ __forceinline__ f32x2_t e4m3x2_to_f32(uint32_t d) {
+  return __builtin_amdgcn_cvt_pk_f32_fp8((int)d, WORD_HI);
 }
 
 // OCP e4m3fn byte -> fp32, exact (bias 7, no infinities, S.1111.111 = NaN).

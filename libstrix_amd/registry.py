@@ -312,13 +312,13 @@ KERNELS: list[Kernel] = [
     Kernel(
         "fp8_wmma_gemm_cfg",
         "fp8_tile_sweep",
-        "fp8_wmma_gemm pinned to one tile config (0..5)",
+        "fp8_wmma_gemm pinned to one tile config (0..7)",
         {"weight_bits": 8, "weight_dtype": "fp8_e4m3", "group_size": (0, 128), "dtype": "bf16"},
     ),
     Kernel(
         "fp8_wmma_gemm_raw_cfg",
         "fp8_tile_sweep",
-        "fp8_wmma_gemm_raw pinned to one tile config (0..5)",
+        "fp8_wmma_gemm_raw pinned to one tile config (0..7)",
         {"weight_bits": 8, "weight_dtype": "fp8_e4m3", "group_size": (0, 128), "dtype": "fp16"},
     ),
     Kernel(

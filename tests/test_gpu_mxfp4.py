@@ -50,7 +50,7 @@ def test_gemm_matches_oracle(m, n, k):
     assert peak_rel_err(out, ref) <= TOL
 
 
-@pytest.mark.parametrize("cfg", range(6))
+@pytest.mark.parametrize("cfg", range(8))
 def test_every_cfg(cfg):
     w, s = _w(384, 1536, cfg)
     x = torch.randn(70, 1536, generator=torch.Generator().manual_seed(cfg)).to(torch.bfloat16)
@@ -143,6 +143,26 @@ def test_expert_gemm(tokens, block_m, gemm, activation, small_experts):
         ref = act * u_
     assert not torch.isnan(c).any()
     assert peak_rel_err(c, ref) <= TOL
+
+
+@pytest.mark.parametrize("block_m", [64, 128, 256])
+def test_identity_routing_single_expert(block_m):
+    """One expert, slot i = token i, the sorted ids alone in a fresh
+    allocation (no padding ids): the tiled kernels form no address outside
+    the sorted-id range while setting up their copies."""
+    t, n, k = 512, 5760, 2880
+    w, s = _w(n, k, 7)
+    x = torch.randn(t, k, generator=torch.Generator().manual_seed(8)).to(torch.bfloat16)
+    sorted_ids = torch.arange(t, dtype=torch.int32, device=DEV)
+    expert_ids = torch.zeros(t // block_m, dtype=torch.int32, device=DEV)
+    num_post = torch.tensor([t], dtype=torch.int32, device=DEV)
+    c = torch.full((t, n), float("nan"), dtype=torch.bfloat16, device=DEV)
+    torch.ops.strix.moe_gemm_mxfp4(c, x.to(DEV), w[None].to(DEV), s[None].to(DEV), sorted_ids, expert_ids, num_post,
+                                   None, 1, block_m, 64, False, "silu")
+    rows = torch.cat([torch.arange(4), torch.arange(t - 4, t)])
+    ref = x[rows].float() @ oracle.mxfp4_decode(w, s).t()
+    assert not torch.isnan(c).any()
+    assert peak_rel_err(c.cpu()[rows], ref) <= TOL
 
 
 @pytest.fixture(scope="module")

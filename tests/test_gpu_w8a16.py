@@ -68,7 +68,7 @@ def test_fp8_wmma_channel(n, k, raw):
     assert peak_rel_err(out, x.float() @ (w.float() * s[:, None]).t()) <= 8e-3
 
 
-@pytest.mark.parametrize("cfg", range(6))
+@pytest.mark.parametrize("cfg", range(8))
 def test_fp8_wmma_every_cfg(cfg):
     w, bs = make(640, 1536, cfg)
     x = torch.randn(70, 1536, generator=torch.Generator().manual_seed(cfg)).to(torch.bfloat16)
