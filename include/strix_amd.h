@@ -59,6 +59,11 @@ int strix_int8_quant_per_token(const void* x, int x_dtype, int64_t ldx, int8_t* 
  * (csrc/torch_ops.cpp:217, csrc/moe/moe_gemm_w4a8.hip:282-316). */
 int strix_int8_quant_group128(const void* x, int x_dtype, int64_t ldx, int8_t* q, int64_t ldq,
                               float* s, int64_t lds, int64_t M, int64_t K, void* stream);
+/* out[m,k] = q[m,k] * s[m, k/128] in bf16/fp16 (STRIX_BF16/F16): the int8
+ * activations of moe_gemm_w4a8 and w4a8_wmma_gemm (csrc/torch_ops.cpp:214-217, 283),
+ * handed to the 16-bit MFMA GEMMs over the int4 weights. */
+int strix_int8_dequant_group128(const int8_t* q, int64_t ldq, const float* s, int64_t lds, void* out,
+                                int out_dtype, int64_t ldo, int64_t M, int64_t K, void* stream);
 /* e4m3fn per (row, 128-group): s = max|x|/448 (1 if 0), q = e4m3_rne(x/s).
  * Absent in the reference (its FP8 path is W8A16, python/strix_vllm/fp8.py:122-124);
  * the input quant step of vLLM's Fp8BlockScaledMMLinearKernel that strix disables. */
@@ -143,9 +148,23 @@ int strix_mxfp4_gemm(const uint8_t* w, int64_t ldw, const uint8_t* scales, int64
 int strix_fp8_w8a16_gemm(const uint8_t* w, int64_t ldw, const float* scales, int64_t s_ld, int block_scales,
                          const void* x, int x_dtype, int64_t ldx, void* out, int64_t ldo, int out_dtype, int64_t M,
                          int64_t N, int64_t K, int cfg, void* stream);
-/* Whole-matrix dequant to bf16 (mxfp4_dequant, fp8_dequant, csrc/torch_ops.cpp:252, 294):
- * fmt 1 MXFP4, 4 FP8 (kgroup 128 + nblock 128 for block scales, kgroup 0 for channel),
- * 3 INT4 symmetric plain nibbles. */
+/* Dense weight-only GEMM over a packed weight format: out[m,n] = sum_k x[m,k]
+ * decode(w[n,k]) (+ bias, bias_rs 0 = [N]). Scale of (n,k) at
+ * scales[(n/nblock)*s_ns + (k/kgroup)*s_ks] (kgroup 0: one per row), s_kind
+ * 0 f32, 1 bf16, 2 f16, 3 e8m0. fmt: 1 MXFP4, 3 INT4 (q-8) plain nibbles,
+ * 4 e4m3, 5 int8, 6 uint4b8 in the RDNAHybridW4A16 word order (k 0 2 4 6 1 3
+ * 5 7 per nibble), 7 uint8b128. Replaces the weight-only ops
+ * fp8_skinny_gemm, w8a16_skinny_gemm (csrc/torch_ops.cpp:250-255;
+ * csrc/gemm/w8a16_skinny_gemm.hip:525-775), w4a16_wmma_gemm
+ * (csrc/torch_ops.cpp:266-268; csrc/gemm/w4a16_wmma_gemm.hip:1-245) and
+ * mxfp4_gemv (csrc/torch_ops.cpp:293; csrc/gemm/mxfp4_gemv.hip:37-147). */
+int strix_w16_gemm(int fmt, const uint8_t* w, int64_t ldw, const void* scales, int s_kind, int64_t s_ns,
+                   int64_t s_ks, int64_t kgroup, int64_t nblock, const void* x, int x_dtype, int64_t ldx,
+                   const void* bias, int64_t bias_rs, void* out, int64_t ldo, int out_dtype, int64_t M, int64_t N,
+                   int64_t K, int cfg, void* stream);
+/* Whole-matrix dequant to bf16 (mxfp4_dequant, fp8_dequant, w4a16_dequant,
+ * csrc/torch_ops.cpp:252, 294-295): fmt as strix_w16_gemm (1, 3, 4, 5, 6, 7);
+ * FP8 block scales use kgroup 128 + nblock 128, channel scales kgroup 0. */
 int strix_dequant_bf16(int fmt, const uint8_t* w, int64_t ldw, const void* scales, int s_kind, int64_t s_ld,
                        int64_t kgroup, int64_t nblock, uint16_t* out, int64_t ldo, int64_t N, int64_t K, void* stream);
 

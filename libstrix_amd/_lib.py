@@ -28,8 +28,8 @@ MOE16 = [P, L, I, P, L, I, P, L, P, L, P, P, L, L, L, I, I, L, L, P]
 
 # scale dtype codes of the 16-bit GEMMs
 S_F32, S_BF16, S_F16, S_E8M0 = 0, 1, 2, 3
-# weight format codes of strix_dequant_bf16
-FMT_MXFP4, FMT_INT4_SYM, FMT_FP8 = 1, 3, 4
+# weight format codes of strix_w16_gemm / strix_dequant_bf16
+FMT_MXFP4, FMT_INT4_SYM, FMT_FP8, FMT_INT8, FMT_INT4_EX, FMT_U8B128 = 1, 3, 4, 5, 6, 7
 
 # name -> argument types (all return int unless listed in _RESTYPE)
 SIGNATURES: dict[str, list] = {
@@ -38,6 +38,8 @@ SIGNATURES: dict[str, list] = {
     "strix_int8_quant_per_token": [P, I, L, P, L, P, L, L, P],
     "strix_int8_quant_group128": [P, I, L, P, L, P, L, L, L, P],
     "strix_fp8_quant_group128": [P, I, L, P, L, P, L, L, L, P],
+    "strix_int8_dequant_group128": [P, L, P, L, P, I, L, L, L, P],
+    "strix_w16_gemm": [I, P, L, P, I, L, L, L, L, P, I, L, P, L, P, L, I, L, L, L, I, P],
     "strix_fp8_w8a8_block_gemm": [P, L, P, L, P, L, P, L, P, L, I, L, L, L, I, P],
     "strix_w8a8_int8_gemm": [P, L, P, P, L, P, P, L, I, L, L, L, I, P],
     "strix_w8a8_int8_group_gemm": [P, L, P, L, P, L, I, P, L, L, P, L, I, L, L, L, I, P],

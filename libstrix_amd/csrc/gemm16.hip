@@ -35,12 +35,16 @@
 namespace strix {
 namespace {
 
-enum WFmt : int { kWBf16 = 0, kWMxfp4 = 1, kWInt4Zp = 2, kWInt4Sym = 3, kWFp8 = 4, kWInt8 = 5 };
+// kWInt4Ex: uint4b8 (q - 8) in vLLM's RDNAHybridW4A16 order: each little-endian
+// 32-bit word holds 8 consecutive K values, nibble j carrying k = 0 2 4 6 1 3 5 7
+// (csrc/gemm/w4a16_wmma_gemm.hip:1-8, 82-89). kWU8b128: uint8 bytes, value b - 128.
+enum WFmt : int { kWBf16 = 0, kWMxfp4 = 1, kWInt4Zp = 2, kWInt4Sym = 3, kWFp8 = 4, kWInt8 = 5, kWInt4Ex = 6,
+                  kWU8b128 = 7 };
 enum SKind : int { kSF32 = 0, kSBf16 = 1, kSF16 = 2, kSE8m0 = 3 };
 
 template <int FMT>
 struct FmtInfo {
-  static constexpr int bits = (FMT == kWBf16) ? 16 : ((FMT == kWFp8 || FMT == kWInt8) ? 8 : 4);
+  static constexpr int bits = (FMT == kWBf16) ? 16 : ((FMT == kWFp8 || FMT == kWInt8 || FMT == kWU8b128) ? 8 : 4);
 };
 
 struct G16 {
@@ -208,6 +212,21 @@ __device__ __forceinline__ void decode_dword(uint32_t d, float s, float z, uint3
       const float v1 = (float)(int)(int8_t)((d >> (16 * j + 8)) & 0xffu);
       out[j] = pack2<F16>(v0 * s, v1 * s);
     }
+  } else if constexpr (FMT == kWU8b128) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const float v0 = (float)((int)((d >> (16 * j)) & 0xffu) - 128);
+      const float v1 = (float)((int)((d >> (16 * j + 8)) & 0xffu) - 128);
+      out[j] = pack2<F16>(v0 * s, v1 * s);
+    }
+  } else if constexpr (FMT == kWInt4Ex) {
+    // lo bytes hold nibbles 0 2 4 6 (k 0 4 1 5), hi bytes nibbles 1 3 5 7 (k 2 6 3 7).
+    const uint32_t lo = d & 0x0f0f0f0fu, hi = (d >> 4) & 0x0f0f0f0fu;
+    auto f = [&](uint32_t w, int b) { return ((float)((w >> (8 * b)) & 0xffu) - 8.0f) * s; };
+    out[0] = pack2<F16>(f(lo, 0), f(lo, 2));  // k 0, 1
+    out[1] = pack2<F16>(f(hi, 0), f(hi, 2));  // k 2, 3
+    out[2] = pack2<F16>(f(lo, 1), f(lo, 3));  // k 4, 5
+    out[3] = pack2<F16>(f(hi, 1), f(hi, 3));  // k 6, 7
   }
 }
 
@@ -899,13 +918,44 @@ int strix_fp8_w8a16_gemm(const uint8_t* w, int64_t ldw, const float* scales, int
   return run_dense16<kWFp8>(op, p, x, x_dtype, ldx, out, ldo, out_dtype, M, N, K, cfg, stream);
 }
 
+// Dense weight-only GEMM over any packed weight format: out[m, n] =
+// sum_k x[m, k] * decode(w[n, k]) (+ bias), scale of (n, k) at
+// scales[(n / nblock) * s_ns + (k / kgroup) * s_ks] (kgroup 0: one per row group).
+int strix_w16_gemm(int fmt, const uint8_t* w, int64_t ldw, const void* scales, int s_kind, int64_t s_ns,
+                   int64_t s_ks, int64_t kgroup, int64_t nblock, const void* x, int x_dtype, int64_t ldx,
+                   const void* bias, int64_t bias_rs, void* out, int64_t ldo, int out_dtype, int64_t M, int64_t N,
+                   int64_t K, int cfg, void* stream) {
+  const char* op = "w16_gemm";
+  STRIX_REQUIRE(fmt == kWMxfp4 || fmt == kWInt4Sym || fmt == kWFp8 || fmt == kWInt8 || fmt == kWInt4Ex ||
+                    fmt == kWU8b128,
+                "%s: unsupported weight format %d", op, fmt);
+  STRIX_REQUIRE(K % 64 == 0, "%s: K must be a multiple of 64, got K=%lld", op, (long long)K);
+  const int piece = (fmt == kWFp8 || fmt == kWInt8 || fmt == kWU8b128) ? 16 : 32;  // K values sharing a scale read
+  STRIX_REQUIRE(kgroup >= 0 && (kgroup == 0 || (kgroup % piece == 0 && K % kgroup == 0)),
+                "%s: scale group (%lld) must be 0 or a multiple of %d dividing K", op, (long long)kgroup, piece);
+  STRIX_REQUIRE(nblock >= 1, "%s: rows per scale row must be >= 1", op);
+  G16 p = g16_weights(w, 0, ldw, scales, s_kind, 0, s_ns, s_ks, (int)kgroup, (int)nblock);
+  p.bias = static_cast<const uint16_t*>(bias);
+  p.bias_rs = bias_rs;
+  switch (fmt) {
+    case kWMxfp4: return run_dense16<kWMxfp4>(op, p, x, x_dtype, ldx, out, ldo, out_dtype, M, N, K, cfg, stream);
+    case kWInt4Sym: return run_dense16<kWInt4Sym>(op, p, x, x_dtype, ldx, out, ldo, out_dtype, M, N, K, cfg, stream);
+    case kWFp8: return run_dense16<kWFp8>(op, p, x, x_dtype, ldx, out, ldo, out_dtype, M, N, K, cfg, stream);
+    case kWInt8: return run_dense16<kWInt8>(op, p, x, x_dtype, ldx, out, ldo, out_dtype, M, N, K, cfg, stream);
+    case kWInt4Ex: return run_dense16<kWInt4Ex>(op, p, x, x_dtype, ldx, out, ldo, out_dtype, M, N, K, cfg, stream);
+    default: return run_dense16<kWU8b128>(op, p, x, x_dtype, ldx, out, ldo, out_dtype, M, N, K, cfg, stream);
+  }
+}
+
 // Whole-matrix dequant to bf16: fmt 1 MXFP4 (e8m0 scales [N, s_ld]), 4 FP8 (block
 // scales [N/128, s_ld] or channel [N]), 3 INT4 symmetric plain nibbles (group g, scales [N, s_ld]).
 int strix_dequant_bf16(int fmt, const uint8_t* w, int64_t ldw, const void* scales, int s_kind, int64_t s_ld,
                        int64_t kgroup, int64_t nblock, uint16_t* out, int64_t ldo, int64_t N, int64_t K, void* stream) {
   const char* op = fmt == kWMxfp4 ? "mxfp4_dequant" : (fmt == kWFp8 ? "fp8_dequant" : "w4a16_dequant");
-  STRIX_REQUIRE(fmt == kWMxfp4 || fmt == kWFp8 || fmt == kWInt4Sym, "%s: unsupported format %d", op, fmt);
-  const int bits = fmt == kWFp8 ? 8 : 4;
+  STRIX_REQUIRE(fmt == kWMxfp4 || fmt == kWFp8 || fmt == kWInt4Sym || fmt == kWInt4Ex || fmt == kWInt8 ||
+                    fmt == kWU8b128,
+                "%s: unsupported format %d", op, fmt);
+  const int bits = (fmt == kWFp8 || fmt == kWInt8 || fmt == kWU8b128) ? 8 : 4;
   const int pv = 128 / bits;
   STRIX_REQUIRE(K % pv == 0, "%s: K must be a multiple of %d", op, pv);
   STRIX_REQUIRE(aligned(w, 16) && ldw % 16 == 0 && aligned(out, 16) && ldo % 8 == 0, "%s: rows must be 16-byte aligned", op);
@@ -920,9 +970,14 @@ int strix_dequant_bf16(int fmt, const uint8_t* w, int64_t ldw, const void* scale
   const int64_t pieces = N * (K / pv);
   const unsigned blocks = (unsigned)((pieces + 255) / 256);
   hipStream_t st = as_stream(stream);
-  if (fmt == kWMxfp4) hipLaunchKernelGGL(dequant_kernel<kWMxfp4>, dim3(blocks), dim3(256), 0, st, p, out, ldo);
-  else if (fmt == kWFp8) hipLaunchKernelGGL(dequant_kernel<kWFp8>, dim3(blocks), dim3(256), 0, st, p, out, ldo);
-  else hipLaunchKernelGGL(dequant_kernel<kWInt4Sym>, dim3(blocks), dim3(256), 0, st, p, out, ldo);
+  switch (fmt) {
+    case kWMxfp4: hipLaunchKernelGGL(dequant_kernel<kWMxfp4>, dim3(blocks), dim3(256), 0, st, p, out, ldo); break;
+    case kWFp8: hipLaunchKernelGGL(dequant_kernel<kWFp8>, dim3(blocks), dim3(256), 0, st, p, out, ldo); break;
+    case kWInt4Ex: hipLaunchKernelGGL(dequant_kernel<kWInt4Ex>, dim3(blocks), dim3(256), 0, st, p, out, ldo); break;
+    case kWInt8: hipLaunchKernelGGL(dequant_kernel<kWInt8>, dim3(blocks), dim3(256), 0, st, p, out, ldo); break;
+    case kWU8b128: hipLaunchKernelGGL(dequant_kernel<kWU8b128>, dim3(blocks), dim3(256), 0, st, p, out, ldo); break;
+    default: hipLaunchKernelGGL(dequant_kernel<kWInt4Sym>, dim3(blocks), dim3(256), 0, st, p, out, ldo); break;
+  }
   return check_launch(op);
 }
 

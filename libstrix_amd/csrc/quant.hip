@@ -117,6 +117,30 @@ __global__ void __launch_bounds__(256)
   *reinterpret_cast<uint2*>(q + m * ldq + k) = make_uint2(lo, hi);
 }
 
+// out[m, k] = q[m, k] * s[m, k / 128] rounded to the 16-bit output type: the
+// activations an int8 x int4 GEMM multiplies, handed to a 16-bit MFMA GEMM.
+template <bool F16>
+__global__ void __launch_bounds__(256)
+    int8_dequant_group128_kernel(const int8_t* __restrict__ q, int64_t ldq, const float* __restrict__ s,
+                                 int64_t lds, uint16_t* __restrict__ out, int64_t ldo, int chunks_per_row,
+                                 int64_t total_chunks) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= total_chunks) return;
+  const int64_t m = t / chunks_per_row;
+  const int64_t k = (t % chunks_per_row) * 8;
+  const uint2 raw = *reinterpret_cast<const uint2*>(q + m * ldq + k);
+  const float sc = s[m * lds + k / 128];
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t w = i < 2 ? raw.x : raw.y;
+    const float a = (float)(int8_t)((w >> (16 * (i & 1))) & 0xffu) * sc;
+    const float b = (float)(int8_t)((w >> (16 * (i & 1) + 8)) & 0xffu) * sc;
+    o[i] = F16 ? (f32_to_f16_bits(a) | (f32_to_f16_bits(b) << 16)) : pack_bf16x2(a, b);
+  }
+  *reinterpret_cast<u32x4*>(out + m * ldo + k) = u32x4{o[0], o[1], o[2], o[3]};
+}
+
 int check_act(const char* op, const void* x, int x_dtype, int64_t ldx, const void* q, int64_t ldq,
               int64_t M, int64_t K) {
   STRIX_REQUIRE(x_dtype == STRIX_BF16 || x_dtype == STRIX_F16,
@@ -194,6 +218,29 @@ int strix_int8_quant_group128(const void* x, int x_dtype, int64_t ldx, int8_t* q
                               float* s, int64_t lds, int64_t M, int64_t K, void* stream) {
   return quant_group128("int8_quant_group128", false, x, x_dtype, ldx, q, ldq, s, lds, M, K,
                         stream);
+}
+
+int strix_int8_dequant_group128(const int8_t* q, int64_t ldq, const float* s, int64_t lds, void* out,
+                                int out_dtype, int64_t ldo, int64_t M, int64_t K, void* stream) {
+  const char* op = "int8_dequant_group128";
+  STRIX_REQUIRE(out_dtype == STRIX_BF16 || out_dtype == STRIX_F16, "%s: output must be bfloat16 or float16", op);
+  STRIX_REQUIRE(M >= 0 && K >= 0 && K % 128 == 0, "%s: K must be a non-negative multiple of 128", op);
+  STRIX_REQUIRE(ldq >= K && ldq % 8 == 0 && ldo >= K && ldo % 8 == 0, "%s: row strides must be >= K, multiples of 8", op);
+  STRIX_REQUIRE(lds >= K / 128, "%s: scale row stride must be >= K/128", op);
+  STRIX_REQUIRE(M == 0 || (aligned(q, 8) && aligned(out, 16)), "%s: q must be 8-byte and out 16-byte aligned", op);
+  if (M == 0 || K == 0) return STRIX_OK;
+  STRIX_ARCH_GATE();
+  const int cpr = (int)(K / 8);
+  const int64_t total = M * cpr;
+  const unsigned blocks = (unsigned)((total + 255) / 256);
+  uint16_t* o = static_cast<uint16_t*>(out);
+  if (out_dtype == STRIX_F16)
+    hipLaunchKernelGGL(int8_dequant_group128_kernel<true>, dim3(blocks), dim3(256), 0, as_stream(stream), q, ldq,
+                       s, lds, o, ldo, cpr, total);
+  else
+    hipLaunchKernelGGL(int8_dequant_group128_kernel<false>, dim3(blocks), dim3(256), 0, as_stream(stream), q, ldq,
+                       s, lds, o, ldo, cpr, total);
+  return check_launch(op);
 }
 
 int strix_fp8_quant_group128(const void* x, int x_dtype, int64_t ldx, uint8_t* q, int64_t ldq,

@@ -329,6 +329,66 @@ KERNELS: list[Kernel] = [
         {"weight_bits": 8, "weight_dtype": "fp8_e4m3", "group_size": (0, 128), "dtype": "bf16"},
         {"threads": 256},
     ),
+    # ------------------------------------------------------------ weight-only decode ops
+    Kernel(
+        "w8a16_skinny_gemm",
+        "w8a16",
+        "decode GEMM (M <= 8) on the raw uint8b128 weight bytes with per-channel or 32/64/128 group scales in "
+        "the activation dtype: weights decoded to bf16/fp16 in registers, 16x16x32 MFMA, no activation "
+        "quantize. K % 64 == 0",
+        {"weight_bits": 8, "group_size": (0, 32, 64, 128), "rows": Range(hi=8), "dtype": ("bf16", "fp16")},
+        {"kernel": "stream16 (M <= 32 path of strix_w16_gemm)"},
+    ),
+    Kernel(
+        "fp8_skinny_gemm",
+        "fp8",
+        "decode GEMM (M <= 8) on float8_e4m3fn weights with fp32 scales per (row, 128-K block) [N, K/128] or "
+        "per channel [N]; e4m3 -> fp32 with gfx950's v_cvt_pk_f32_fp8, bf16 MFMA. K % 64 == 0",
+        {"weight_bits": 8, "weight_dtype": "fp8_e4m3", "group_size": (0, 128), "rows": Range(hi=8),
+         "dtype": ("bf16", "fp16")},
+        {"kernel": "stream16"},
+    ),
+    Kernel(
+        "mxfp4_gemv",
+        "mxfp4_gemv",
+        "MXFP4 W4A16 for M <= 8: the packed e2m1 stream decoded in registers, one 16-row subtile per wave "
+        "with K split across the block, bf16 MFMA",
+        {"weight_bits": 4, "group_size": 32, "dtype": "bf16", "m_max": 8},
+        {"kernel": "stream16"},
+    ),
+    Kernel(
+        "w4a16_wmma_gemm",
+        "w4a16",
+        "uint4b8 weights in the RDNAHybridW4A16 word order (nibble j of each 32-bit word is k = 0 2 4 6 1 3 5 7) "
+        "with bf16 group scales: decoded to bf16 in registers (M <= 32) or into LDS by producer waves while "
+        "consumer waves run bf16 MFMA (prefill). K % 64 == 0, group % 32 == 0",
+        {"weight_bits": 4, "group_size": (32, 64, 128), "rows": Range(lo=1), "dtype": "bf16",
+         "scale_dtype": "bf16"},
+    ),
+    Kernel(
+        "w4a16_dequant",
+        "w4a16_dequant",
+        "RDNAHybridW4A16 int4 [N, K/2] + bf16 group scales -> bf16 [N, K], exact bf16 of (u4 - 8) * scale",
+        {"weight_bits": 4, "group_size": (32, 64, 128), "dtype": "bf16"},
+        {"threads": 256},
+    ),
+    Kernel(
+        "w4a8_wmma_gemm",
+        "w4a16",
+        "uint4b8 RDNAHybridW4A16 weights x activations quantized to int8 per (row, 128-group) in the op: the "
+        "int8 activations are dequantized to bf16 and the weights decoded to bf16 for bf16 MFMA. "
+        "K % 128 == 0, weight group 0, 32 or 128",
+        {"weight_bits": 4, "group_size": (0, 32, 128), "rows": Range(lo=1), "dtype": "bf16"},
+    ),
+    Kernel(
+        "moe_gemm_w4a8",
+        "moe_gemm_w4a8",
+        "expert GEMM over the WNA16 int4 layout (low nibble = even k, q - 8, bf16/fp16 scales per 128-K group) "
+        "with int8 activations per (row, 128-group): activations dequantized to bf16, then the int4 "
+        "bf16-MFMA grouped GEMM with the fused act*mul / top-k weight epilogues",
+        {"silu_mul": True, **_BF16, "activation_dtype": "int8", "weight_dtype": "uint8", "weight_bits": 4,
+         "quant": "wna16", "group_size": (128,), "activation": ("silu", "gelu_tanh"), **_MOE_TILES},
+    ),
 ]
 
 _selections: dict[tuple, dict[str, Any]] = {}

@@ -811,3 +811,253 @@ def _cvt_probe(scales, bf16_in):
 def _(scales, bf16_in):
     return (scales.new_empty((scales.numel(), 4, 256, 2), dtype=torch.int16), scales.new_empty((256,)),
             bf16_in.new_empty((bf16_in.numel(),), dtype=torch.int16))
+
+
+# ----------------------------------------------------------------- weight-only decode / ExLlama int4 / W4A8
+# All of these run on strix_w16_gemm: the packed weights are decoded to
+# bf16/fp16 in registers (decode M) or LDS (prefill M) and contracted with
+# 16-bit MFMA. CuCount arguments are accepted for schema compatibility; the
+# gfx950 kernels size their grids themselves.
+def _w16(fmt, w, x, scales, s_kind, s_ns, s_ks, kgroup, nblock, bias, cfg=-1):
+    n, m, k = w.size(0), x.size(0), x.size(1)
+    out = torch.empty((m, n), dtype=x.dtype, device=x.device)
+    bias_rs = 0
+    if bias is not None:
+        _check(bias.dtype == x.dtype, "bias must have the activation dtype")
+        if bias.dim() == 2:
+            _check(tuple(bias.shape) == (m, n) and bias.stride(1) == 1, "bias must be [N] or [M, N]")
+            bias_rs = bias.stride(0)
+        else:
+            _check(bias.numel() == n, "bias must be [N] or [M, N]")
+            bias = bias.contiguous()
+    _lib.call("strix_w16_gemm", fmt, _ptr(w), w.stride(0), _ptr(scales), s_kind, s_ns, s_ks, kgroup, nblock, _ptr(x),
+              _act_code(x), x.stride(0), _ptr(bias), bias_rs, _ptr(out), n, _act_code(out), m, n, k, cfg, _stream(x))
+    return out
+
+
+def _skinny_rows(x, name="w8a16_skinny_gemm"):
+    _check(1 <= x.size(0) <= 8, f"{name} takes 1-8 rows, got {x.size(0)}")
+
+
+# Reference schema: csrc/torch_ops.cpp:250-252 (csrc/gemm/w8a16_skinny_gemm.hip:525-766).
+@_define(
+    "w8a16_skinny_gemm(Tensor in_a, Tensor in_b, Tensor in_scale, "
+    "Tensor? in_bias, int CuCount, int group_size) -> Tensor"
+)
+def w8a16_skinny_gemm(in_a, in_b, in_scale, in_bias, CuCount, group_size):
+    _check(in_a.dim() == 2 and in_b.dim() == 2, "Weights must be [N, K] and activations [M, K]")
+    _check(in_a.dtype == torch.uint8, f"Weights must be uint8 (uint8b128), got {in_a.dtype}")
+    _check(in_b.dtype in (torch.float16, torch.bfloat16), "Activation must be float16 or bfloat16")
+    _check(in_scale.dtype == in_b.dtype, "Scale dtype must match activation dtype")
+    _check(group_size in (0, 32, 64, 128), f"group_size must be 0 (per-channel), 32, 64, or 128, got {group_size}")
+    n, k = in_a.shape
+    _check(in_b.size(1) == k and in_b.stride(1) == 1 and in_a.stride(1) == 1, "K mismatch or non-contiguous rows")
+    _skinny_rows(in_b)
+    if group_size:
+        _check(k % group_size == 0, f"K must be divisible by group_size={group_size}")
+        _check(in_scale.dim() == 2 and tuple(in_scale.shape) == (n, k // group_size) and in_scale.stride(1) == 1,
+               f"Scale must be [{n}, {k // group_size}] but got {list(in_scale.shape)}")
+        s_ns, s_ks = in_scale.stride(0), 1
+    else:
+        _check(in_scale.dim() == 1 and in_scale.numel() == n, f"Per-channel scale must be [{n}]")
+        in_scale = in_scale.contiguous()
+        s_ns, s_ks = 1, 0
+    return _w16(_lib.FMT_U8B128, in_a, in_b, in_scale, _SCALE_KIND[in_scale.dtype], s_ns, s_ks, group_size, 1,
+                in_bias)
+
+
+@_fake("w8a16_skinny_gemm")
+def _(in_a, in_b, in_scale, in_bias, CuCount, group_size):
+    return in_b.new_empty((in_b.size(0), in_a.size(0)))
+
+
+# Reference schema: csrc/torch_ops.cpp:253-255: e4m3 weights, fp32 scales per
+# row [N] or per (row, 128-K block) [N, K/128].
+@_define(
+    "fp8_skinny_gemm(Tensor in_a, Tensor in_b, Tensor in_scale, "
+    "Tensor? in_bias, int CuCount) -> Tensor"
+)
+def fp8_skinny_gemm(in_a, in_b, in_scale, in_bias, CuCount):
+    _check(in_a.dim() == 2 and in_b.dim() == 2, "Weights must be [N, K] and activations [M, K]")
+    _check(in_a.dtype == torch.float8_e4m3fn, f"Weights must be float8_e4m3fn, got {in_a.dtype}")
+    _check(in_b.dtype in (torch.float16, torch.bfloat16), "Activation must be float16 or bfloat16")
+    _check(in_scale.dtype == torch.float32, "fp8 scales must be float32")
+    n, k = in_a.shape
+    _check(in_b.size(1) == k and in_b.stride(1) == 1 and in_a.stride(1) == 1, "K mismatch or non-contiguous rows")
+    _skinny_rows(in_b)
+    if in_scale.dim() == 2:
+        _check(tuple(in_scale.shape) == (n, k // 128) and in_scale.stride(1) == 1 and k % 128 == 0,
+               f"Scale must be [{n}, {k // 128}] but got {list(in_scale.shape)}")
+        s_ns, s_ks, kgroup = in_scale.stride(0), 1, 128
+    else:
+        _check(in_scale.numel() == n, f"Per-channel scale must be [{n}]")
+        in_scale = in_scale.contiguous()
+        s_ns, s_ks, kgroup = 1, 0, 0
+    return _w16(_lib.FMT_FP8, in_a.view(torch.uint8), in_b, in_scale, _lib.S_F32, s_ns, s_ks, kgroup, 1, in_bias)
+
+
+@_fake("fp8_skinny_gemm")
+def _(in_a, in_b, in_scale, in_bias, CuCount):
+    return in_b.new_empty((in_b.size(0), in_a.size(0)))
+
+
+# Reference schema: csrc/torch_ops.cpp:293 (csrc/gemm/mxfp4_gemv.hip:110-147).
+@_define("mxfp4_gemv(Tensor x, Tensor w, Tensor scales) -> Tensor")
+def mxfp4_gemv(x, w, scales):
+    _check(x.dtype == torch.bfloat16 and x.dim() == 2 and x.stride(1) == 1 and x.stride(0) % 8 == 0,
+           "x must be bf16 [M, K] with 16-byte aligned rows")
+    _check(w.dtype == torch.uint8 and w.dim() == 2 and w.stride(1) == 1 and w.stride(0) % 16 == 0,
+           "w must be uint8 [N, K/2] with 16-byte aligned rows")
+    m, k = x.shape
+    n = w.size(0)
+    _check(1 <= m <= 8, "mxfp4_gemv is for M <= 8")
+    _check(w.size(1) * 2 == k and k % 32 == 0, "K mismatch or K % 32")
+    _check(scales.dtype == torch.uint8 and tuple(scales.shape) == (n, k // 32) and scales.stride(1) == 1,
+           "scales must be uint8 [N, K/32]")
+    return _w16(_lib.FMT_MXFP4, w, x, scales, _lib.S_E8M0, scales.stride(0), 1, 32, 1, None)
+
+
+@_fake("mxfp4_gemv")
+def _(x, w, scales):
+    return x.new_empty((x.size(0), w.size(0)))
+
+
+def _int4_ex_checks(w, n_scales, k, group_size, scales):
+    _check(w.dtype in (torch.int8, torch.uint8) and w.dim() == 2 and w.stride(1) == 1 and w.stride(0) % 8 == 0,
+           "w must be int8 [N, K/2] (RDNAHybridW4A16 words) with 8-byte aligned rows")
+    _check(w.size(1) * 2 == k and k % 64 == 0, "K mismatch or K % 64")
+    _check(group_size % 32 == 0 and k % group_size == 0, "group_size % 32 and K % group")
+    _check(scales.dtype == torch.bfloat16 and scales.dim() == 2 and tuple(scales.shape) == (n_scales, k // group_size)
+           and scales.stride(1) == 1, "scales must be bf16 [N, K / group_size]")
+
+
+# Reference schema: csrc/torch_ops.cpp:266-268: uint4b8 weights in the
+# RDNAHybridW4A16 word order, bf16 group scales, optional bf16 bias.
+@_define("w4a16_wmma_gemm(Tensor x, Tensor w, Tensor scales, Tensor? bias, int group_size) -> Tensor")
+def w4a16_wmma_gemm(x, w, scales, bias, group_size):
+    _check(x.dtype == torch.bfloat16 and x.dim() == 2 and x.stride(1) == 1 and x.stride(0) % 8 == 0,
+           "x must be bf16 [M, K] with 16-byte aligned rows")
+    m, k = x.shape
+    n = w.size(0)
+    _int4_ex_checks(w, n, k, group_size, scales)
+    if bias is not None:
+        _check(bias.dtype == torch.bfloat16 and bias.numel() == n, "bias")
+    return _w16(_lib.FMT_INT4_EX, w.view(torch.uint8), x, scales, _lib.S_BF16, scales.stride(0), 1, group_size, 1,
+                bias)
+
+
+@_fake("w4a16_wmma_gemm")
+def _(x, w, scales, bias, group_size):
+    return x.new_empty((x.size(0), w.size(0)))
+
+
+# Reference schema: csrc/torch_ops.cpp:295: bf16 of (u4 - 8) * scale, exact.
+@_define("w4a16_dequant(Tensor w, Tensor scales, int group_size) -> Tensor")
+def w4a16_dequant(w, scales, group_size):
+    n, k = w.size(0), 2 * w.size(1)
+    _int4_ex_checks(w, n, k, group_size, scales)
+    out = torch.empty((n, k), dtype=torch.bfloat16, device=w.device)
+    _lib.call("strix_dequant_bf16", _lib.FMT_INT4_EX, _ptr(w), w.stride(0), _ptr(scales), _lib.S_BF16,
+              scales.stride(0), group_size, 1, _ptr(out), k, n, k, _stream(w))
+    return out
+
+
+@_fake("w4a16_dequant")
+def _(w, scales, group_size):
+    return w.new_empty((w.size(0), 2 * w.size(1)), dtype=torch.bfloat16)
+
+
+# Reference schema: csrc/torch_ops.cpp:283: uint4b8 RDNAHybridW4A16 weights,
+# activations quantized to int8 per (row, 128-group) inside the op, fp32
+# weight scales [N] (one group) or [G, N] / [N, G]. The int8 activations are
+# dequantized (q * s, bf16) and contracted with the decoded weights on bf16 MFMA.
+@_define("w4a8_wmma_gemm(Tensor in_w4, Tensor in_act, Tensor in_scale) -> Tensor")
+def w4a8_wmma_gemm(in_w4, in_act, in_scale):
+    _check(in_act.dim() == 2 and in_act.dtype == torch.bfloat16, "Activation must be bf16 [M, K]")
+    m, k = in_act.shape
+    n = in_w4.size(0)
+    _check(in_w4.dim() == 2 and in_w4.dtype in (torch.int8, torch.uint8) and in_w4.stride(1) == 1
+           and 2 * in_w4.size(1) == k, "Weights must be int8 [N, K/2]")
+    _check(k % 128 == 0, f"K must be divisible by 128, got K={k}")
+    _check(in_scale.dtype == torch.float32, f"Scale must be float32, got {in_scale.dtype}")
+    if in_scale.dim() == 1:
+        _check(in_scale.numel() == n, f"Per-channel scale must be [N={n}]")
+        scale, s_ns, s_ks, group = in_scale.contiguous(), 1, 0, 0
+    else:
+        g = in_scale.size(0) if in_scale.size(1) == n else in_scale.size(1)
+        _check(g >= 1 and k % g == 0, "Scale must be [G, N], [N, G] or [N]")
+        group = k // g
+        if tuple(in_scale.shape) == (g, n) and in_scale.stride(1) == 1:
+            scale, s_ns, s_ks = in_scale, 1, in_scale.stride(0)
+        else:
+            _check(tuple(in_scale.shape) == (n, g) and in_scale.stride(1) == 1,
+                   f"Scale must be [G, N], [N, G] or [N={n}] but got {list(in_scale.shape)}")
+            scale, s_ns, s_ks = in_scale, in_scale.stride(0), 1
+        _check(group % 32 == 0, f"weight group ({group}) must be a multiple of 32")
+    x = in_act.contiguous()
+    q = torch.empty((m, k), dtype=torch.int8, device=x.device)
+    sa = torch.empty((m, k // 128), dtype=torch.float32, device=x.device)
+    xd = torch.empty((m, k), dtype=torch.bfloat16, device=x.device)
+    st = _stream(x)
+    if m:
+        _lib.call("strix_int8_quant_group128", _ptr(x), _act_code(x), k, _ptr(q), k, _ptr(sa), k // 128, m, k, st)
+        _lib.call("strix_int8_dequant_group128", _ptr(q), k, _ptr(sa), k // 128, _ptr(xd), _lib.BF16, k, m, k, st)
+    return _w16(_lib.FMT_INT4_EX, in_w4.view(torch.uint8), xd, scale, _lib.S_F32, s_ns, s_ks, group, 1, None)
+
+
+@_fake("w4a8_wmma_gemm")
+def _(in_w4, in_act, in_scale):
+    return in_act.new_empty((in_act.size(0), in_w4.size(0)))
+
+
+# Reference schema: csrc/torch_ops.cpp:213-217: int8 activations per (row,
+# 128-group) (moe_act_quant_i8) x int4 experts in the WNA16 layout (uint8
+# [E, N, K/2], low nibble = even k, value q - 8) with bf16/fp16 scales per
+# 128-K group. The activations are dequantized (q * s, bf16) and the experts
+# run on the int4 bf16-MFMA grouped GEMM.
+@_define(
+    "moe_gemm_w4a8(Tensor(a!) c, Tensor qa, Tensor sa, Tensor b, Tensor scales, "
+    "Tensor sorted_ids, Tensor expert_ids, Tensor num_post_padded, "
+    "Tensor? topk_weights, int top_k, int block_m, int block_n, "
+    "bool silu_mul=False, str activation='silu') -> ()"
+)
+def moe_gemm_w4a8(c, qa, sa, b, scales, sorted_ids, expert_ids, num_post_padded, topk_weights, top_k, block_m,
+                  block_n, silu_mul=False, activation="silu"):
+    _check(qa.dtype == torch.int8 and qa.dim() == 2 and qa.stride(1) == 1, "qa must be int8 [rows, K]")
+    rows, k = qa.shape
+    _check(k % 128 == 0, f"K must be a multiple of 128, got K={k}")
+    _check(sa.dtype == torch.float32 and tuple(sa.shape) == (rows, k // 128) and sa.stride(1) == 1,
+           "sa must be float32 [rows, K/128]")
+    _check(c.dtype == torch.bfloat16, "c must be bfloat16")
+    a = torch.empty((rows, k), dtype=torch.bfloat16, device=qa.device)
+    if rows:
+        _lib.call("strix_int8_dequant_group128", _ptr(qa), qa.stride(0), _ptr(sa), sa.stride(0), _ptr(a), _lib.BF16,
+                  k, rows, k, _stream(qa))
+    moe_gemm_w4a16(c, a, b, scales, sorted_ids, expert_ids, num_post_padded, topk_weights, top_k, block_m, block_n,
+                   silu_mul, activation, 128)
+
+
+@_fake("moe_gemm_w4a8")
+def _(c, qa, sa, b, scales, sorted_ids, expert_ids, num_post_padded, topk_weights, top_k, block_m, block_n,
+      silu_mul=False, activation="silu"):
+    return None
+
+
+# Reference schema: csrc/torch_ops.cpp:183 (the fragment-layout probe of
+# tests/test_wmma_layout.py): D[16,16] = A[16,K] . B[16,K]^T in fp32 through
+# the bf16 MFMA. K is zero-padded to the MFMA's 32.
+@_define("_wmma_bf16_tile(Tensor a, Tensor b) -> Tensor")
+def _wmma_bf16_tile(a, b):
+    _check(a.dim() == 2 and a.shape == b.shape and a.size(0) == 16 and a.dtype == b.dtype == torch.bfloat16,
+           "a, b must be bf16 [16, K]")
+    k = a.size(1)
+    kp = -(-k // 32) * 32
+    if kp != k:
+        a = torch.nn.functional.pad(a, (0, kp - k))
+        b = torch.nn.functional.pad(b, (0, kp - k))
+    return _mfma_tile(a, b)
+
+
+@_fake("_wmma_bf16_tile")
+def _(a, b):
+    return a.new_empty((16, 16), dtype=torch.float32)

@@ -19,6 +19,10 @@ inputs, or invariants chosen so that a plausible mistake fails; see the
 
 from oracle.quant import (  # noqa: F401
     e4m3_decode,
+    u8b128_decode,
+    wna16_ex_decode,
+    wna16_ex_pack,
+    wna16_ex_unpack,
     fp8_quant_group128,
     int8_quant_group128,
     int8_quant_per_token,

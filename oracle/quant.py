@@ -114,3 +114,54 @@ def wna16_zp_decode(qweight: torch.Tensor, scales: torch.Tensor, zeros: torch.Te
     zn = zn.reshape(*z.shape[:-2], z.shape[-2] * 2, z.shape[-1]).float()
     s = scales.detach().to("cpu").float()
     return (q - zn.repeat_interleave(group, dim=-1)) * s.repeat_interleave(group, dim=-1)
+
+
+# nibble j of each 32-bit word holds k = EX_ORDER[j] of its 8 consecutive k
+EX_ORDER = (0, 2, 4, 6, 1, 3, 5, 7)
+
+
+def wna16_ex_pack(q: torch.Tensor) -> torch.Tensor:
+    """uint4 values [.., N, K] -> the RDNAHybridW4A16 int8 [.., N, K/2] view of
+    ExLlama-shuffled int32 words: little-endian words of 8 consecutive k,
+    nibble j = k EX_ORDER[j] (csrc/gemm/w4a16_wmma_gemm.hip:1-8, 82-89; the
+    reference tests build it with vLLM's pack_skinny_int4, tests/test_w8a16.py:74-95).
+    Pinned by: tests/test_oracle_quant.py (hand-packed known word, inverse of
+    wna16_ex_decode)."""
+    q = q.detach().to("cpu").to(torch.int64)
+    *lead, k = q.shape
+    g = q.reshape(*lead, k // 8, 8)
+    word = torch.zeros(*lead, k // 8, dtype=torch.int64)
+    for j, kk in enumerate(EX_ORDER):
+        word |= (g[..., kk] & 15) << (4 * j)
+    b = torch.stack([(word >> (8 * i)) & 0xFF for i in range(4)], dim=-1).reshape(*lead, k // 2)
+    return b.to(torch.uint8).view(torch.int8)
+
+
+def wna16_ex_unpack(w: torch.Tensor) -> torch.Tensor:
+    """Inverse of wna16_ex_pack: int8/uint8 [.., N, K/2] -> uint4 [.., N, K]."""
+    b = w.detach().to("cpu").view(torch.uint8).to(torch.int64)
+    *lead, k2 = b.shape
+    word = b.reshape(*lead, k2 // 4, 4)
+    word = word[..., 0] | (word[..., 1] << 8) | (word[..., 2] << 16) | (word[..., 3] << 24)
+    q = torch.zeros(*lead, k2 // 4, 8, dtype=torch.int64)
+    for j, kk in enumerate(EX_ORDER):
+        q[..., kk] = (word >> (4 * j)) & 15
+    return q.reshape(*lead, k2 * 2)
+
+
+def wna16_ex_decode(w: torch.Tensor, scales: torch.Tensor, group: int) -> torch.Tensor:
+    """(u4 - 8) * scale in fp32 for the RDNAHybridW4A16 layout, scales
+    [.., N, K/group] (tests/test_w8a16.py:102-119). Pinned by:
+    tests/test_oracle_quant.py."""
+    q = wna16_ex_unpack(w).float()
+    return (q - 8.0) * scales.detach().to("cpu").float().repeat_interleave(group, dim=-1)
+
+
+def u8b128_decode(w_u8: torch.Tensor, scales: torch.Tensor, group: int) -> torch.Tensor:
+    """uint8b128 weights [N, K]: (b - 128) * scale, scales [N] (group 0) or
+    [N, K/group] (tests/test_w8a16.py:9-17). Pinned by: tests/test_oracle_quant.py."""
+    w = w_u8.detach().to("cpu").to(torch.float32) - 128.0
+    s = scales.detach().to("cpu").float()
+    if group:
+        return w * s.repeat_interleave(group, dim=-1)[..., : w.shape[-1]]
+    return w * s.reshape(-1, 1)

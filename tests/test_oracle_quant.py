@@ -151,3 +151,24 @@ def test_wna16_sym_decode_nibble_order():
     w = torch.tensor([[[0x9A]]], dtype=torch.uint8)  # k=0: 10, k=1: 9
     s = torch.tensor([[[2.0]]], dtype=torch.bfloat16)
     assert oracle.wna16_sym_decode(w, s, 2).tolist() == [[[4.0, 2.0]]]
+
+
+def test_wna16_ex_pack_known_word_and_inverse():
+    # k = 0..7 with value k: nibble j must hold k (0 2 4 6 1 3 5 7)[j], so the
+    # little-endian word is 0x75316420 -> bytes 20 64 31 75.
+    q = torch.arange(8).reshape(1, 8)
+    b = oracle.wna16_ex_pack(q).view(torch.uint8)
+    assert b.tolist() == [[0x20, 0x64, 0x31, 0x75]]
+    g = torch.Generator().manual_seed(3)
+    q = torch.randint(0, 16, (5, 64), generator=g)
+    assert torch.equal(oracle.wna16_ex_unpack(oracle.wna16_ex_pack(q)), q)
+    s = torch.rand(5, 2, generator=g)
+    d = oracle.wna16_ex_decode(oracle.wna16_ex_pack(q), s, 32)
+    assert torch.equal(d, (q.float() - 8) * s.repeat_interleave(32, 1))
+
+
+def test_u8b128_decode_channel_and_group():
+    w = torch.tensor([[0, 128, 255, 129]], dtype=torch.uint8)
+    assert oracle.u8b128_decode(w, torch.tensor([2.0]), 0).tolist() == [[-256.0, 0.0, 254.0, 2.0]]
+    s = torch.tensor([[1.0, 0.5]])
+    assert oracle.u8b128_decode(w, s, 2).tolist() == [[-128.0, 0.0, 63.5, 0.5]]
