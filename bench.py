@@ -103,7 +103,8 @@ def headline(torch, S, timer, steps, warmup):
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_FP8_TFLOPS, 4),
             "traffic": None,
-            "kernel": "tiled8_kernel<fp8 block, 256x256>",
+            "kernel": "tiled8_kernel<fp8 block>: 256x256 rounds + 128x128 strip of the leftover columns "
+                      "(two launches per GEMM call, timed together)",
             "algorithmic_flops_per_launch": flops,
             "avg_launch_us": round(us_gemm, 2),
         },
@@ -279,6 +280,8 @@ def main() -> None:
     traffic = traffic_from_profile()
     if traffic:
         roof["traffic"] = traffic.get("bytes_per_launch")
+        roof["traffic_source"] = ("profiles/fp8_w8a8_block_gemm_m4096_traffic.json: rocprofv3 FETCH_SIZE + WRITE_SIZE, "
+                                  "scaled by a 1 GiB copy kernel")
     out = {
         "metric": "quant GEMM TFLOP/s %MFMA peak (M≥256); HBM GB/s %peak (M≤16)",
         "value": round(h["value"], 1),
