@@ -60,6 +60,37 @@ class Timer:
         return a.elapsed_time(b) * 1e3 / iters  # us
 
 
+def graph_us(torch, fns, reps: int = 10) -> float:
+    """Per-call time of `fns` (one call each, in order) replayed from one HIP
+    graph: what a serving loop that captures its decode step sees, without
+    per-launch host overhead (the reference's microbenchmarks replay graphs
+    the same way, bench/kernels/w8a8_gemm.py:41-58)."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for f in fns:
+            f()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for f in fns:
+            f()
+    for _ in range(3):
+        g.replay()
+    torch.cuda.synchronize()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        g.replay()
+    b.record()
+    torch.cuda.synchronize()
+    us = a.elapsed_time(b) * 1e3 / (reps * len(fns))
+    del g
+    return us
+
+
 def fp8_bytes(m, n, k):
     return n * k + ((n + 127) // 128) * (k // 128) * 4 + m * k * 2 + m * n * 2
 
@@ -139,6 +170,9 @@ def point_c2(torch, S, timer, m, weights):
            "tflops": round(flops / us_k / 1e6, 1), "gbs": round(by / us_k / 1e3, 1),
            "frac_fp8_mfma": round(flops / us_k / 1e6 / PEAK_FP8_TFLOPS, 4),
            "frac_hbm": round(by / us_k / 1e3 / PEAK_HBM_GBS, 4), "cold_weight_sets": len(sets)}
+    if m <= 16:
+        fns = [lambda w=w, sw=sw: S.fp8_w8a8_block_gemm(*S.fp8_quant_group128(x), w, sw) for (w, sw) in sets]
+        res["op_graph_us"] = round(graph_us(torch, fns), 2)
     del sets
     return res
 
@@ -197,9 +231,13 @@ def point_c3(torch, S, timer, t, c3):
     ids, _ = S.moe_route_topk(ls[0], top_k, True)
     by, touched = moe_bytes_fp8(ids, h, inter, t, h, e)
     flops = 2.0 * t * top_k * (2 * inter * h + h * inter)
-    return {"T": t, "op_us": round(us, 2), "tflops": round(flops / us / 1e6, 2), "gbs": round(by / us / 1e3, 1),
-            "frac_fp8_mfma": round(flops / us / 1e6 / PEAK_FP8_TFLOPS, 4),
-            "frac_hbm": round(by / us / 1e3 / PEAK_HBM_GBS, 4), "experts_touched": touched}
+    res = {"T": t, "op_us": round(us, 2), "tflops": round(flops / us / 1e6, 2), "gbs": round(by / us / 1e3, 1),
+           "frac_fp8_mfma": round(flops / us / 1e6 / PEAK_FP8_TFLOPS, 4),
+           "frac_hbm": round(by / us / 1e3 / PEAK_HBM_GBS, 4), "experts_touched": touched}
+    if t <= 64:
+        gu = graph_us(torch, [lambda j=j: op(j) for j in range(nsets)])
+        res.update({"op_graph_us": round(gu, 2), "frac_hbm_graph": round(by / gu / 1e3 / PEAK_HBM_GBS, 4)})
+    return res
 
 
 def point_moe16(torch, S, timer, name, t, d, run, bytes_per_expert, e, top_k, h, inter):
@@ -213,9 +251,13 @@ def point_moe16(torch, S, timer, name, t, d, run, bytes_per_expert, e, top_k, h,
     touched = int(ids.unique().numel())
     by = touched * bytes_per_expert + t * h * 2 * 2 + t * e * 4
     flops = 2.0 * t * top_k * (2 * inter * h + h * inter)
-    return {"T": t, "op_us": round(us, 2), "tflops": round(flops / us / 1e6, 2), "gbs": round(by / us / 1e3, 1),
-            "frac_bf16_mfma": round(flops / us / 1e6 / PEAK_BF16_TFLOPS, 4),
-            "frac_hbm": round(by / us / 1e3 / PEAK_HBM_GBS, 4), "experts_touched": touched, "config": name}
+    res = {"T": t, "op_us": round(us, 2), "tflops": round(flops / us / 1e6, 2), "gbs": round(by / us / 1e3, 1),
+           "frac_bf16_mfma": round(flops / us / 1e6 / PEAK_BF16_TFLOPS, 4),
+           "frac_hbm": round(by / us / 1e3 / PEAK_HBM_GBS, 4), "experts_touched": touched, "config": name}
+    if t <= 64:
+        gu = graph_us(torch, [lambda j=j: run(xs[j], ls[j]) for j in range(nsets)])
+        res.update({"op_graph_us": round(gu, 2), "frac_hbm_graph": round(by / gu / 1e3 / PEAK_HBM_GBS, 4)})
+    return res
 
 
 def cpu_baseline(torch):
@@ -255,8 +297,8 @@ def traffic_from_profile():
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-points", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()

@@ -182,6 +182,15 @@ int64_t strix_moe_align_workspace_bytes(int64_t num_slots, int64_t E);
 int strix_moe_align(const int32_t* topk_ids, int64_t num_slots, int64_t E, int64_t block_m,
                     int32_t* sorted_ids, int64_t sorted_cap, int32_t* expert_ids, int64_t blocks_cap,
                     int32_t* num_post, void* workspace, int64_t workspace_bytes, void* stream);
+/* Router and align in one call: the reference runs vLLM's fused_topk then
+ * moe_align_block_size (python/strix_vllm/moe.py:181-184, 286-288). Same
+ * outputs as strix_moe_route_topk (ldo = top_k) followed by strix_moe_align;
+ * up to 1024 slots (T * top_k) both run in one single-block kernel launch.
+ * Workspace: strix_moe_align_workspace_bytes(T * top_k, E). */
+int strix_moe_route_align(const void* logits, int logits_dtype, int64_t ldl, int64_t T, int64_t E, int64_t top_k,
+                          int renormalize, int32_t* topk_ids, float* topk_weights, int64_t block_m,
+                          int32_t* sorted_ids, int64_t sorted_cap, int32_t* expert_ids, int64_t blocks_cap,
+                          int32_t* num_post, void* workspace, int64_t workspace_bytes, void* stream);
 /* moe_sum (python/strix_vllm/moe.py:328-330): out[t] = sum_j w[t,j] * y[t*k+j]
  * (w NULL = unweighted), fp32 in slot order. */
 int strix_moe_sum(const void* y, int dtype, int64_t ldy, int64_t T, int64_t top_k, int64_t H,

@@ -793,10 +793,13 @@ __global__ void __launch_bounds__(WM * WN * 64) tiled8_kernel(G8 p, int tiles_m,
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) prev_sw[i] = cur_sw[i];
-        if (s + 1 < NT) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        // The next fragment's reads go out after this subtile's first MFMA:
+        // the wait for them then comes one subtile later, never right after
+        // they are issued.
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
           __builtin_amdgcn_sched_group_barrier(0x008, KIND == kFp8Block ? 1 : 2, 0);
+          if (t == 0 && s + 1 < NT) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
           if (s > 0) __builtin_amdgcn_sched_group_barrier(0x002, KIND == kFp8Block ? 4 : 8, 0);
         }
       }
@@ -930,10 +933,15 @@ template <int KIND, int EPI, bool WX128>
 int dense_dispatch(const G8& p, hipStream_t st, const char* op, int cfg) {
   const int M = p.M;
   if (cfg < 0) {
+    // Decode streams the weights through a per-wave LDS ring. Above that the
+    // tile shape is the largest whose tile count still fills the chip: 256x256
+    // once it covers every CU, 128x256 (three stages) below that, and 128x128
+    // up to 128 rows, where the wider tiles leave most CUs idle.
+    const int64_t t256 = (int64_t)((M + 255) / 256) * ((p.n_out + 255) / 256);
     if (M <= 32) cfg = 0;
-    else if (M <= 64) cfg = 2;
-    else if (M <= 512) cfg = 3;
-    else cfg = 5;
+    else if (M <= 128) cfg = 3;
+    else if (t256 >= cu_count()) cfg = 5;
+    else cfg = 6;
   }
   switch (cfg) {
     case 0: return launch_ring<KIND, 1, false, EPI, kActSilu, 5, WX128, 1>(p, (M + 15) / 16, st, op);

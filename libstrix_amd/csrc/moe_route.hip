@@ -19,14 +19,12 @@ namespace {
 
 constexpr int kMaxExpertsPerLane = 16;  // E <= 1024
 
-// One wave per token.
+// Top-k of one token's logits by one wave. Lane r < k ends with the r-th
+// selected expert in `my_id` and its weight in the return value.
 template <bool BF16_LOGITS>
-__global__ void __launch_bounds__(256)
-    route_topk_kernel(const void* __restrict__ logits, int64_t ldl, int T, int E, int k, int renorm,
-                      int32_t* __restrict__ ids, float* __restrict__ wts, int64_t ldo) {
+__device__ __forceinline__ float route_token(const void* __restrict__ logits, int64_t ldl, int t, int E, int k,
+                                             int renorm, int& my_id) {
   const int lane = threadIdx.x & 63;
-  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (t >= T) return;
   float v[kMaxExpertsPerLane];
   const int per = (E + 63) / 64;
 #pragma unroll
@@ -56,7 +54,7 @@ __global__ void __launch_bounds__(256)
   uint32_t taken = 0;  // bit j: element j of this lane already selected
   float sel_sum = 0.0f;
   float my_e = 0.0f;   // lane r keeps exp(sel_r - mx)
-  int my_id = 0;
+  my_id = 0;
   for (int r = 0; r < k; ++r) {
     float bv = -INFINITY;
     int bi = 0x7fffffff;
@@ -78,10 +76,136 @@ __global__ void __launch_bounds__(256)
     sel_sum += ev;
     if (lane == r) { my_e = ev; my_id = bi; }
   }
+  return renorm ? my_e / sel_sum : my_e / denom_all;
+}
+
+// One wave per token.
+template <bool BF16_LOGITS>
+__global__ void __launch_bounds__(256)
+    route_topk_kernel(const void* __restrict__ logits, int64_t ldl, int T, int E, int k, int renorm,
+                      int32_t* __restrict__ ids, float* __restrict__ wts, int64_t ldo) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  int my_id = 0;
+  const float w = route_token<BF16_LOGITS>(logits, ldl, t, E, k, renorm, my_id);
   if (lane < k) {
     ids[(int64_t)t * ldo + lane] = my_id;
-    wts[(int64_t)t * ldo + lane] = renorm ? my_e / sel_sum : my_e / denom_all;
+    wts[(int64_t)t * ldo + lane] = w;
   }
+}
+
+// ---- align, small case: every step in one block of 1024 threads, the slot
+// ids in LDS. Used up to kAlignSmall slots (decode and small prefill), where
+// the three-pass path below is all launch latency.
+constexpr int kAlignSmall = 1024;
+
+// Inclusive sum over the block of one value per thread (1024 threads).
+__device__ __forceinline__ int block_inclusive_sum(int x, int* wave_tot) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o, kWave);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) wave_tot[wave] = x;
+  __syncthreads();
+  if (threadIdx.x < 16) {
+    int v = wave_tot[threadIdx.x];
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) {
+      const int y = __shfl_up(v, o, kWave);
+      if ((int)threadIdx.x >= o) v += y;
+    }
+    wave_tot[threadIdx.x] = v;
+  }
+  __syncthreads();
+  return x + (wave > 0 ? wave_tot[wave - 1] : 0);
+}
+
+// Align the S slot ids held in LDS `ids` (S <= 1024, E <= 1024). Same outputs
+// as the three-pass path: stable within an expert, runs padded with S.
+__device__ void align_block(const int32_t* ids, int S, int E, int block_m, int32_t* __restrict__ sorted_ids,
+                            int64_t sorted_cap, int32_t* __restrict__ expert_ids, int64_t blocks_cap,
+                            int32_t* __restrict__ num_post, int* cnt, int* off, int* wave_tot) {
+  const int tid = threadIdx.x;
+  if (tid < E) cnt[tid] = 0;
+  __syncthreads();
+  if (tid < S) {
+    const int e = ids[tid];
+    if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+  }
+  __syncthreads();
+  const int c = tid < E ? cnt[tid] : 0;
+  const int padded = (c + block_m - 1) / block_m * block_m;
+  const int incl = block_inclusive_sum(padded, wave_tot);
+  if (tid < E) off[tid] = incl - padded;
+  const int total = wave_tot[15];
+  if (tid == 0) num_post[0] = total;
+  __syncthreads();
+  // Padding: each expert's tail and everything past the last run.
+  if (tid < E) {
+    for (int i = c; i < padded; ++i) sorted_ids[off[tid] + i] = S;
+  }
+  for (int64_t i = total + tid; i < sorted_cap; i += 1024) sorted_ids[i] = S;
+  for (int64_t b = tid; b < blocks_cap; b += 1024) {
+    int ex = -1;
+    const int64_t pos = b * block_m;
+    if (pos < total) {
+      int lo = 0, hi = E - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (off[mid] <= pos) lo = mid; else hi = mid - 1;
+      }
+      while (lo < E - 1 && off[lo + 1] == off[lo]) ++lo;  // skip experts with no slots
+      ex = lo;
+    }
+    expert_ids[b] = ex;
+  }
+  // Stable scatter: rank = earlier slots of the same expert.
+  if (tid < S) {
+    const int e = ids[tid];
+    if (e >= 0 && e < E) {
+      int rank = 0;
+      for (int j = 0; j < tid; ++j) rank += (ids[j] == e);
+      sorted_ids[off[e] + rank] = tid;
+    }
+  }
+}
+
+__global__ void __launch_bounds__(1024)
+    align_small_kernel(const int32_t* __restrict__ topk_ids, int S, int E, int block_m,
+                       int32_t* __restrict__ sorted_ids, int64_t sorted_cap, int32_t* __restrict__ expert_ids,
+                       int64_t blocks_cap, int32_t* __restrict__ num_post) {
+  __shared__ int32_t ids[kAlignSmall];
+  __shared__ int cnt[1024], off[1024], wave_tot[16];
+  if ((int)threadIdx.x < S) ids[threadIdx.x] = topk_ids[threadIdx.x];
+  __syncthreads();
+  align_block(ids, S, E, block_m, sorted_ids, sorted_cap, expert_ids, blocks_cap, num_post, cnt, off, wave_tot);
+}
+
+// Router and align in one block: 16 waves route the T tokens (T * k <= 1024),
+// then the block aligns the slot ids it just produced.
+template <bool BF16_LOGITS>
+__global__ void __launch_bounds__(1024)
+    route_align_small_kernel(const void* __restrict__ logits, int64_t ldl, int T, int E, int k, int renorm,
+                             int32_t* __restrict__ topk_ids, float* __restrict__ topk_w, int block_m,
+                             int32_t* __restrict__ sorted_ids, int64_t sorted_cap, int32_t* __restrict__ expert_ids,
+                             int64_t blocks_cap, int32_t* __restrict__ num_post) {
+  __shared__ int32_t ids[kAlignSmall];
+  __shared__ int cnt[1024], off[1024], wave_tot[16];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int t = wave; t < T; t += 16) {
+    int my_id = 0;
+    const float w = route_token<BF16_LOGITS>(logits, ldl, t, E, k, renorm, my_id);
+    if (lane < k) {
+      ids[t * k + lane] = my_id;
+      topk_ids[(int64_t)t * k + lane] = my_id;
+      topk_w[(int64_t)t * k + lane] = w;
+    }
+  }
+  __syncthreads();
+  align_block(ids, T * k, E, block_m, sorted_ids, sorted_cap, expert_ids, blocks_cap, num_post, cnt, off, wave_tot);
 }
 
 // ---- align, pass 1: per-chunk histograms. Chunk c covers slots [256c, 256c+256).
@@ -100,29 +224,53 @@ __global__ void __launch_bounds__(256)
 }
 
 // ---- align, pass 2 (one block): expert offsets, per-chunk bases (in place
-// over hist), expert_ids, num_post_padded and the padding fill.
+// over hist), expert_ids, num_post_padded and the padding fill. Thread
+// (part, e) owns expert e's chunks [part*cpp, (part+1)*cpp): its loads are
+// independent and coalesced across e, and the only serial step is a block
+// scan over the E padded counts.
 __global__ void __launch_bounds__(1024)
     align_scan_kernel(int32_t* __restrict__ hist, int chunks, int S, int E, int block_m,
                       int32_t* __restrict__ sorted_ids, int64_t sorted_cap, int32_t* __restrict__ expert_ids,
                       int64_t blocks_cap, int32_t* __restrict__ num_post) {
-  extern __shared__ int32_t sm[];  // [E] padded counts, then [E] offsets
-  int32_t* padded = sm;
-  int32_t* off = sm + E;
-  for (int e = threadIdx.x; e < E; e += 1024) {
-    int cnt = 0;
-    for (int c = 0; c < chunks; ++c) cnt += hist[(int64_t)c * E + e];
-    padded[e] = (cnt + block_m - 1) / block_m * block_m;
+  extern __shared__ int32_t sm[];  // [parts][E] partial counts, then [E] offsets, [16] wave totals
+  const int parts = max(1, 1024 / E);
+  const int cpp = (chunks + parts - 1) / parts;
+  int32_t* psum = sm;
+  int32_t* off = sm + parts * E;
+  int32_t* wave_tot = off + E;
+  const int tid = threadIdx.x;
+  const int e = tid % E, part = tid / E;
+  const bool owner = part < parts && tid < parts * E;
+  const int c0 = owner ? part * cpp : 0, c1 = owner ? min(chunks, c0 + cpp) : 0;
+  // Experts beyond 1024 threads: one thread walks several (E > 1024 is rejected on the host).
+  int local = 0;
+  {
+    int c = c0;
+    for (; c + 4 <= c1; c += 4) {
+      const int a = hist[(int64_t)c * E + e], b = hist[(int64_t)(c + 1) * E + e];
+      const int d = hist[(int64_t)(c + 2) * E + e], f = hist[(int64_t)(c + 3) * E + e];
+      local += a + b + d + f;
+    }
+    for (; c < c1; ++c) local += hist[(int64_t)c * E + e];
   }
+  if (owner) psum[part * E + e] = local;
   __syncthreads();
-  if (threadIdx.x == 0) {  // E <= 1024: a serial scan is a few microseconds at most
-    int run = 0;
-    for (int e = 0; e < E; ++e) { off[e] = run; run += padded[e]; }
-    num_post[0] = run;
+  int cnt = 0;
+  if (tid < E)
+    for (int q = 0; q < parts; ++q) cnt += psum[q * E + tid];
+  const int padded = tid < E ? (cnt + block_m - 1) / block_m * block_m : 0;
+  const int incl = block_inclusive_sum(padded, wave_tot);
+  if (tid < E) off[tid] = incl - padded;
+  const int total = wave_tot[15];
+  if (tid == 0) num_post[0] = total;
+  __syncthreads();
+  // Padding fill: each expert's tail, then everything past the last run
+  // (disjoint from the slots the scatter pass writes).
+  if (tid < E) {
+    for (int i = cnt; i < padded; ++i) sorted_ids[off[tid] + i] = S;
   }
-  __syncthreads();
-  const int total = off[E - 1] + padded[E - 1];
-  for (int64_t i = threadIdx.x; i < sorted_cap; i += 1024) sorted_ids[i] = S;
-  for (int64_t b = threadIdx.x; b < blocks_cap; b += 1024) {
+  for (int64_t i = total + tid; i < sorted_cap; i += 1024) sorted_ids[i] = S;
+  for (int64_t b = tid; b < blocks_cap; b += 1024) {
     int ex = -1;
     const int64_t pos = b * block_m;
     if (pos < total) {  // binary search: last expert whose offset <= pos
@@ -131,15 +279,16 @@ __global__ void __launch_bounds__(1024)
         const int mid = (lo + hi + 1) >> 1;
         if (off[mid] <= pos) lo = mid; else hi = mid - 1;
       }
-      // Experts with zero slots share the offset of the next; skip to the one that owns pos.
-      while (lo < E - 1 && padded[lo] == 0) ++lo;
+      while (lo < E - 1 && off[lo + 1] == off[lo]) ++lo;  // skip experts with no slots
       ex = lo;
     }
     expert_ids[b] = ex;
   }
-  for (int e = threadIdx.x; e < E; e += 1024) {
+  // Chunk bases: expert offset + this part's predecessors + running count.
+  if (owner) {
     int run = off[e];
-    for (int c = 0; c < chunks; ++c) {
+    for (int q = 0; q < part; ++q) run += psum[q * E + e];
+    for (int c = c0; c < c1; ++c) {
       const int64_t i = (int64_t)c * E + e;
       const int n = hist[i];
       hist[i] = run;
@@ -250,17 +399,56 @@ int strix_moe_align(const int32_t* topk_ids, int64_t num_slots, int64_t E, int64
   STRIX_ARCH_GATE();
   hipStream_t st = as_stream(stream);
   const int S = (int)num_slots;
-  const int chunks = S > 0 ? (S + 255) / 256 : 1;
+  if (S <= kAlignSmall) {
+    hipLaunchKernelGGL(align_small_kernel, dim3(1), dim3(1024), 0, st, topk_ids, S, (int)E, (int)block_m, sorted_ids,
+                       sorted_cap, expert_ids, blocks_cap, num_post);
+    return check_launch(op);
+  }
+  const int chunks = (S + 255) / 256;
   int32_t* hist = static_cast<int32_t*>(workspace);
   hipLaunchKernelGGL(align_hist_kernel, dim3(chunks), dim3(256), (size_t)E * 4, st, topk_ids, S, (int)E, hist);
   int rc = check_launch(op);
   if (rc) return rc;
-  hipLaunchKernelGGL(align_scan_kernel, dim3(1), dim3(1024), (size_t)E * 8, st, hist, chunks, S, (int)E,
+  const int parts = (int)std::max<int64_t>(1, 1024 / E);
+  const size_t scan_lds = ((size_t)parts * E + E + 16) * 4;
+  hipLaunchKernelGGL(align_scan_kernel, dim3(1), dim3(1024), scan_lds, st, hist, chunks, S, (int)E,
                      (int)block_m, sorted_ids, sorted_cap, expert_ids, blocks_cap, num_post);
   rc = check_launch(op);
   if (rc) return rc;
-  if (S == 0) return STRIX_OK;
   hipLaunchKernelGGL(align_scatter_kernel, dim3(chunks), dim3(256), 0, st, topk_ids, S, (int)E, hist, sorted_ids);
+  return check_launch(op);
+}
+
+int strix_moe_route_align(const void* logits, int logits_dtype, int64_t ldl, int64_t T, int64_t E, int64_t top_k,
+                          int renormalize, int32_t* topk_ids, float* topk_weights, int64_t block_m,
+                          int32_t* sorted_ids, int64_t sorted_cap, int32_t* expert_ids, int64_t blocks_cap,
+                          int32_t* num_post, void* workspace, int64_t workspace_bytes, void* stream) {
+  const char* op = "moe_route_align";
+  if (T * top_k > kAlignSmall || T == 0) {
+    int rc = strix_moe_route_topk(logits, logits_dtype, ldl, T, E, top_k, renormalize, topk_ids, topk_weights, top_k,
+                                  stream);
+    if (rc) return rc;
+    return strix_moe_align(topk_ids, T * top_k, E, block_m, sorted_ids, sorted_cap, expert_ids, blocks_cap, num_post,
+                           workspace, workspace_bytes, stream);
+  }
+  STRIX_REQUIRE(logits_dtype == STRIX_F32 || logits_dtype == STRIX_BF16, "%s: logits must be float32 or bfloat16", op);
+  STRIX_REQUIRE(E >= 1 && E <= 64 * kMaxExpertsPerLane, "%s: 1 <= E <= %d, got E=%lld", op,
+                64 * kMaxExpertsPerLane, (long long)E);
+  STRIX_REQUIRE(top_k >= 1 && top_k <= 64 && top_k <= E, "%s: 1 <= top_k <= min(E, 64), got %lld", op,
+                (long long)top_k);
+  STRIX_REQUIRE(ldl >= E, "%s: bad logits stride", op);
+  STRIX_REQUIRE(block_m >= 1 && block_m <= 1024, "%s: block_m must be in 1..1024", op);
+  STRIX_REQUIRE(sorted_cap >= strix_moe_align_sorted_capacity(T * top_k, E, block_m), "%s: sorted_ids too small", op);
+  STRIX_REQUIRE(blocks_cap * block_m >= sorted_cap, "%s: expert_ids needs ceil(capacity / block_m) entries", op);
+  STRIX_ARCH_GATE();
+  if (logits_dtype == STRIX_BF16)
+    hipLaunchKernelGGL(route_align_small_kernel<true>, dim3(1), dim3(1024), 0, as_stream(stream), logits, ldl, (int)T,
+                       (int)E, (int)top_k, renormalize, topk_ids, topk_weights, (int)block_m, sorted_ids, sorted_cap,
+                       expert_ids, blocks_cap, num_post);
+  else
+    hipLaunchKernelGGL(route_align_small_kernel<false>, dim3(1), dim3(1024), 0, as_stream(stream), logits, ldl,
+                       (int)T, (int)E, (int)top_k, renormalize, topk_ids, topk_weights, (int)block_m, sorted_ids,
+                       sorted_cap, expert_ids, blocks_cap, num_post);
   return check_launch(op);
 }
 

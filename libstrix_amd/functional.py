@@ -43,9 +43,8 @@ def moe_block_m(tokens: int, top_k: int, num_experts: int) -> int:
 
 
 def route_and_align(logits: torch.Tensor, top_k: int, num_experts: int, block_m: int, renormalize: bool = True):
-    ids, w = S.moe_route_topk(logits, top_k, renormalize)
-    sorted_ids, expert_ids, num_post = S.moe_align(ids, num_experts, block_m)
-    return ids, w, sorted_ids, expert_ids, num_post
+    """Router top-k and the expert alignment (one launch up to 1024 slots)."""
+    return S.moe_route_align(logits, top_k, block_m, renormalize)
 
 
 def fused_moe_fp8_w8a8(x, logits, w13, w13_s, w2, w2_s, top_k: int, renormalize: bool = True,

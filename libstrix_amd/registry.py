@@ -182,10 +182,30 @@ KERNELS: list[Kernel] = [
     ),
     Kernel(
         "moe_align",
+        "moe_align_small",
+        "moe_align_block_size contract in one 1024-thread block: LDS histogram, block scan, stable "
+        "scatter by rank (up to 1024 slots)",
+        {"num_experts": Range(lo=1, hi=1024), "num_slots": Range(hi=1024)},
+    ),
+    Kernel(
+        "moe_align",
         "moe_align",
         "moe_align_block_size contract: stable counting sort of slot ids by expert (bit-exact, no "
         "atomics on global memory), each expert padded to block_m with id T*top_k",
         {"num_experts": Range(lo=1, hi=1024)},
+    ),
+    Kernel(
+        "moe_route_align",
+        "moe_route_align_small",
+        "router top-k and align in one 1024-thread block launch (T * top_k <= 1024); the same outputs "
+        "as moe_route_topk then moe_align",
+        {"logits_dtype": ("fp32", "bf16"), "num_experts": Range(hi=1024), "num_slots": Range(hi=1024)},
+    ),
+    Kernel(
+        "moe_route_align",
+        "moe_route_then_align",
+        "moe_route_topk then the three-pass moe_align (more than 1024 slots)",
+        {"logits_dtype": ("fp32", "bf16"), "num_experts": Range(hi=1024)},
     ),
     Kernel(
         "moe_sum",

@@ -359,6 +359,39 @@ def _(topk_ids, num_experts, block_m):
     return (topk_ids.new_empty((cap,)), topk_ids.new_empty((nblk,)), topk_ids.new_empty((1,)))
 
 
+# Extension: the router and the align as one op (T * top_k <= 1024 runs as
+# one single-block kernel); same outputs as moe_route_topk then moe_align.
+@_define("moe_route_align(Tensor logits, int top_k, int block_m, bool renormalize=True) "
+         "-> (Tensor, Tensor, Tensor, Tensor, Tensor)")
+def moe_route_align(logits, top_k, block_m, renormalize=True):
+    _rowmajor(logits, "logits")
+    _check(logits.dtype in (torch.float32, torch.bfloat16), "logits must be float32 or bfloat16")
+    t, e = logits.shape
+    dev = logits.device
+    ids = torch.empty((t, top_k), dtype=torch.int32, device=dev)
+    w = torch.empty((t, top_k), dtype=torch.float32, device=dev)
+    cap, nblk = align_capacity(t * top_k, e, block_m)
+    sorted_ids = torch.empty((cap,), dtype=torch.int32, device=dev)
+    expert_ids = torch.empty((nblk,), dtype=torch.int32, device=dev)
+    num_post = torch.empty((1,), dtype=torch.int32, device=dev)
+    ws_bytes = _lib.query("strix_moe_align_workspace_bytes", t * top_k, e)
+    ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev)
+    code = _lib.F32 if logits.dtype == torch.float32 else _lib.BF16
+    _lib.call("strix_moe_route_align", _ptr(logits), code, logits.stride(0), t, e, top_k, int(bool(renormalize)),
+              _ptr(ids), _ptr(w), block_m, _ptr(sorted_ids), cap, _ptr(expert_ids), nblk, _ptr(num_post), _ptr(ws),
+              ws_bytes, _stream(logits))
+    return ids, w, sorted_ids, expert_ids, num_post
+
+
+@_fake("moe_route_align")
+def _(logits, top_k, block_m, renormalize=True):
+    t, e = logits.shape
+    cap, nblk = align_capacity(t * top_k, e, block_m)
+    i32 = torch.int32
+    return (logits.new_empty((t, top_k), dtype=i32), logits.new_empty((t, top_k), dtype=torch.float32),
+            logits.new_empty((cap,), dtype=i32), logits.new_empty((nblk,), dtype=i32), logits.new_empty((1,), dtype=i32))
+
+
 def _sum_impl(inp, weights, output):
     _check(inp.dim() == 3 and inp.is_contiguous(), "input must be contiguous [T, top_k, H]")
     t, k, h = inp.shape

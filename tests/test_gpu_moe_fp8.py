@@ -57,6 +57,37 @@ def test_align_bit_exact(t, k, e, bm):
     assert (x[total // bm:] == -1).all()
 
 
+@pytest.mark.parametrize("s,e,bm", [(1024, 128, 16), (1025, 128, 16), (1000, 1024, 64), (1024, 96, 32),
+                                    (3000, 1000, 128), (2049, 7, 16), (0, 8, 16)])
+def test_align_single_block_threshold_bit_exact(s, e, bm):
+    """Up to 1024 slots the align runs as one block, above as three passes:
+    both against the contract, with uneven E, empty experts and no slots."""
+    g = torch.Generator().manual_seed(s + e)
+    ids = torch.randint(0, e, (s,), generator=g, dtype=torch.int32)
+    if s:
+        ids[ids == 1] = 2          # expert 1 never routed
+    sorted_ids, expert_ids, num_post = torch.ops.strix.moe_align(ids.to(DEV), e, bm)
+    rs, re, total = oracle.align(ids, bm, e)
+    assert int(num_post.item()) == total
+    assert sorted_ids.cpu()[:total].tolist() == rs and (sorted_ids.cpu()[total:] == s).all()
+    assert expert_ids.cpu()[:total // bm].tolist() == re and (expert_ids.cpu()[total // bm:] == -1).all()
+
+
+@pytest.mark.parametrize("t,e,k,bm", [(1, 128, 8, 16), (64, 128, 8, 16), (128, 128, 8, 64), (129, 128, 8, 64),
+                                      (3, 32, 4, 32), (300, 1000, 3, 16)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_route_align_matches_route_then_align(t, e, k, bm, dtype):
+    logits = torch.randn(t, e, generator=torch.Generator().manual_seed(t * e + k)).to(dtype)
+    ids, w, sorted_ids, expert_ids, num_post = torch.ops.strix.moe_route_align(logits.to(DEV), k, bm, True)
+    rid, rw = oracle.route_topk(logits.float(), k, True)
+    assert torch.equal(ids.cpu(), rid)
+    torch.testing.assert_close(w.cpu(), rw, rtol=1e-5, atol=1e-7)
+    rs, re, total = oracle.align(rid, bm, e)
+    assert int(num_post.item()) == total and sorted_ids.cpu()[:total].tolist() == rs
+    assert (sorted_ids.cpu()[total:] == t * k).all()
+    assert expert_ids.cpu()[:total // bm].tolist() == re and (expert_ids.cpu()[total // bm:] == -1).all()
+
+
 def test_moe_sum_bit_exact():
     y = torch.randn(37, 8, 2048, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16)
     out = torch.empty(37, 2048, dtype=torch.bfloat16, device=DEV)
