@@ -185,7 +185,8 @@ int strix_moe_align(const int32_t* topk_ids, int64_t num_slots, int64_t E, int64
 /* Router and align in one call: the reference runs vLLM's fused_topk then
  * moe_align_block_size (python/strix_vllm/moe.py:181-184, 286-288). Same
  * outputs as strix_moe_route_topk (ldo = top_k) followed by strix_moe_align;
- * up to 1024 slots (T * top_k) both run in one single-block kernel launch.
+ * up to 16 tokens and 1024 slots (T * top_k) both run in one single-block
+ * kernel launch.
  * Workspace: strix_moe_align_workspace_bytes(T * top_k, E). */
 int strix_moe_route_align(const void* logits, int logits_dtype, int64_t ldl, int64_t T, int64_t E, int64_t top_k,
                           int renormalize, int32_t* topk_ids, float* topk_weights, int64_t block_m,

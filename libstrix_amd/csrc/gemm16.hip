@@ -278,58 +278,117 @@ __global__ void __launch_bounds__(WAVES * 64) stream16_kernel(G16 p) {
 #pragma unroll
     for (int t = 0; t < MT; ++t) acc[s][t] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  auto chunk = [&](int c, auto pv_tag) {
-    constexpr int V = decltype(pv_tag)::value;  // K values per lane in this chunk
-    constexpr int STEPS = V / 8;
-    const int kc = c * CK + g4 * V;            // this lane's first K position
-    uint32_t wv[NT][V / 2];                    // decoded 16-bit pairs
+  // One chunk's MFMAs from its decoded weights and token rows.
+  auto mfmas = [&](const uint32_t (&wv)[NT][PV / 2], const u32x4 (&av)[MT][PV / 8], auto steps_tag) {
+    constexpr int STEPS = decltype(steps_tag)::value;
 #pragma unroll
-    for (int s = 0; s < NT; ++s) {
-      const uint8_t* src = wbase + (int64_t)wrow[s] * p.ldw + (int64_t)kc * BITS / 8;
-      if constexpr (FMT == kWBf16) {
-        const u32x4 raw = ldg128(src);
+    for (int t = 0; t < MT; ++t)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) wv[s][i] = raw[i];
-      } else {
-        uint32_t raw[V * BITS / 32];
-        if constexpr (V * BITS == 128) {
-          const u32x4 r4 = ldg128(src);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) raw[i] = r4[i];
-        } else {
-          const uint2 r2 = *reinterpret_cast<const uint2*>(src);
-          raw[0] = r2.x;
-          raw[1] = r2.y;
-        }
-        const float sc = wscale(p, expert, wrow[s], kc);
-        const float z = (FMT == kWInt4Zp) ? wzero(p, expert, wrow[s], kc) : 8.0f;
-        constexpr int PAIRS_PER_DWORD = 32 / BITS / 2;
-#pragma unroll
-        for (int i = 0; i < V * BITS / 32; ++i) decode_dword<FMT, F16>(raw[i], sc, z, &wv[s][i * PAIRS_PER_DWORD]);
-      }
-    }
-#pragma unroll
-    for (int t = 0; t < MT; ++t) {
-      const uint16_t* ar = p.a + (int64_t)brow[t] * p.lda + kc;
-#pragma unroll
-      for (int j = 0; j < STEPS; ++j) {
-        const u32x4 av = ldg128(ar + 8 * j);
+      for (int j = 0; j < STEPS; ++j)
 #pragma unroll
         for (int s = 0; s < NT; ++s) {
           u32x4 wq;
 #pragma unroll
           for (int i = 0; i < 4; ++i) wq[i] = wv[s][4 * j + i];
           if constexpr (F16)
-            acc[s][t] = mfma_f16(__builtin_bit_cast(f16x8, wq), __builtin_bit_cast(f16x8, av), acc[s][t]);
+            acc[s][t] = mfma_f16(__builtin_bit_cast(f16x8, wq), __builtin_bit_cast(f16x8, av[t][j]), acc[s][t]);
           else
-            acc[s][t] = mfma_bf16(__builtin_bit_cast(bf16x8, wq), __builtin_bit_cast(bf16x8, av), acc[s][t]);
+            acc[s][t] = mfma_bf16(__builtin_bit_cast(bf16x8, wq), __builtin_bit_cast(bf16x8, av[t][j]), acc[s][t]);
+        }
+  };
+  constexpr bool HAS_S = (FMT != kWBf16);
+  constexpr bool ZP = (FMT == kWInt4Zp);
+  int64_t srow[NT], zrow[NT];
+#pragma unroll
+  for (int s = 0; s < NT; ++s) {
+    srow[s] = HAS_S ? wscale_row(p, expert, wrow[s]) : 0;
+    zrow[s] = ZP ? wzero_row(p, expert, wrow[s]) : 0;
+  }
+  // Decodes raw dwords with the raw scale / zero bits of each subtile.
+  auto decode = [&](const uint32_t* raw, int ndw, int s, uint32_t sbits, uint32_t zbits, uint32_t* wv) {
+    if constexpr (FMT == kWBf16) {
+      for (int i = 0; i < ndw; ++i) wv[i] = raw[i];
+    } else {
+      if constexpr (FMT == kWMxfp4 && !F16) {
+        // e8m0 scales: bf16 by table (v_perm), the scalar path only for the
+        // rare exponents the table cannot take. A lane's dwords share a scale.
+        if (p.ws_kind == kSE8m0 && mxfp4_lut_ok(sbits)) {
+          const Mxfp4Lut t = mxfp4_lut(sbits);
+#pragma unroll
+          for (int i = 0; i < ndw; ++i) mxfp4_dword_lut(raw[i], t, &wv[4 * i]);
+          return;
         }
       }
+      const float sc = wscale_value(p, sbits);
+      const float z = ZP ? (float)((wrow[s] & 1) ? ((zbits >> 4) & 15u) : (zbits & 15u)) : 8.0f;
+      constexpr int PAIRS_PER_DWORD = 32 / BITS / 2;
+#pragma unroll
+      for (int i = 0; i < ndw; ++i) decode_dword<FMT, F16>(raw[i], sc, z, &wv[i * PAIRS_PER_DWORD]);
     }
   };
-  for (int c = c0; c < c1; ++c) {
-    if (FMT != kWBf16 && BITS == 4 && tail && c == nfull) chunk(c, std::integral_constant<int, PV / 2>{});
-    else chunk(c, std::integral_constant<int, PV>{});
+  // Full chunks run as a two-deep register pipeline: the raw weights, raw
+  // scale bits and token rows of chunk c+1 are in flight while chunk c is
+  // decoded and multiplied. Every load is issued unconditionally (the index
+  // is clamped to the wave's last chunk), so each wait counts exactly the
+  // loads of the later chunk.
+  struct Buf {
+    uint32_t w[NT][4];
+    uint32_t s[NT], z[NT];
+    u32x4 a[MT][PV / 8];
+  };
+  auto load = [&](int c, Buf& b) {
+    const int kc = c * CK + g4 * PV;
+#pragma unroll
+    for (int s = 0; s < NT; ++s) {
+      const u32x4 r4 = ldg128(wbase + (int64_t)wrow[s] * p.ldw + (int64_t)kc * BITS / 8);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) b.w[s][i] = r4[i];
+      if constexpr (HAS_S) b.s[s] = wscale_raw(p, srow[s], kc);
+      if constexpr (ZP) b.z[s] = wzero_raw(p, zrow[s], kc);
+    }
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      const uint16_t* ar = p.a + (int64_t)brow[t] * p.lda + kc;
+#pragma unroll
+      for (int j = 0; j < PV / 8; ++j) b.a[t][j] = ldg128(ar + 8 * j);
+    }
+  };
+  auto compute = [&](const Buf& b) {
+    uint32_t wv[NT][PV / 2];
+#pragma unroll
+    for (int s = 0; s < NT; ++s) decode(b.w[s], 4, s, HAS_S ? b.s[s] : 0u, ZP ? b.z[s] : 0u, wv[s]);
+    mfmas(wv, b.a, std::integral_constant<int, PV / 8>{});
+  };
+  const int f1 = min(c1, nfull);
+  if (c0 < f1) {
+    Buf A, B;
+    load(c0, A);
+    for (int c = c0; c < f1; c += 2) {
+      load(min(c + 1, f1 - 1), B);
+      compute(A);
+      if (c + 1 >= f1) break;
+      load(min(c + 2, f1 - 1), A);
+      compute(B);
+    }
+  }
+  // A 4-bit K that is 64 mod 128 ends with a half chunk (8 bytes per lane).
+  if constexpr (FMT != kWBf16 && BITS == 4) {
+    if (tail && c1 == nch && c0 < c1) {
+      const int kc = nfull * CK + g4 * (PV / 2);
+      uint32_t wv[NT][PV / 2];
+#pragma unroll
+      for (int s = 0; s < NT; ++s) {
+        const uint2 r2 = *reinterpret_cast<const uint2*>(wbase + (int64_t)wrow[s] * p.ldw + (int64_t)kc * BITS / 8);
+        const uint32_t raw[2] = {r2.x, r2.y};
+        decode(raw, 2, s, wscale_raw(p, srow[s], kc), ZP ? wzero_raw(p, zrow[s], kc) : 0u, wv[s]);
+      }
+      u32x4 av[MT][PV / 8];
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int j = 0; j < PV / 16; ++j) av[t][j] = ldg128(p.a + (int64_t)brow[t] * p.lda + kc + 8 * j);
+      mfmas(wv, av, std::integral_constant<int, PV / 16>{});
+    }
   }
 
   constexpr int TILES = NT * MT;

@@ -19,76 +19,144 @@ namespace {
 
 constexpr int kMaxExpertsPerLane = 16;  // E <= 1024
 
+// Per-wave LDS scratch of the router: the k selected entries.
+struct RouteScratch {
+  uint32_t key[64];
+  int id[64];
+  float val[64];
+};
+
+// Order-preserving unsigned key of a float (-0 is keyed as +0, so the two
+// tie like the reference's sort does).
+__device__ __forceinline__ uint32_t float_key(float x) {
+  const uint32_t b = __float_as_uint(x + 0.0f);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
 // Top-k of one token's logits by one wave. Lane r < k ends with the r-th
-// selected expert in `my_id` and its weight in the return value.
-template <bool BF16_LOGITS>
+// selected expert (by logit, larger first, lower expert id first on ties) in
+// `my_id` and its softmax weight as the return value.
+//
+// The k-th largest key comes from a 32-step bisection over the key bits,
+// each step one ballot per lane slot; the entries above it and the first
+// ties by expert id are compacted (in expert order) into LDS, ranked there,
+// and permuted into rank order. No step is a k-round argmax.
+//
+// PER = logits per lane (E <= 64 * PER): the loops are unrolled to exactly
+// that, which keeps the code small; a kernel this short is bound by its own
+// instruction fetch more than by its arithmetic.
+template <bool BF16_LOGITS, int PER>
 __device__ __forceinline__ float route_token(const void* __restrict__ logits, int64_t ldl, int t, int E, int k,
-                                             int renorm, int& my_id) {
+                                             int renorm, int& my_id, RouteScratch& sc) {
   const int lane = threadIdx.x & 63;
+  const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));  // lanes below this one
+  constexpr int kMaxExpertsPerLane = PER;
   float v[kMaxExpertsPerLane];
-  const int per = (E + 63) / 64;
+  uint32_t key[kMaxExpertsPerLane];
+  const int per = PER;
 #pragma unroll
   for (int j = 0; j < kMaxExpertsPerLane; ++j) {
     const int e = lane + 64 * j;
     float x = -INFINITY;
-    if (j < per && e < E) {
+    const bool in = j < per && e < E;
+    if (in) {
       if constexpr (BF16_LOGITS)
         x = bf16_bits_to_f32(static_cast<const uint16_t*>(logits)[(int64_t)t * ldl + e]);
       else
         x = static_cast<const float*>(logits)[(int64_t)t * ldl + e];
     }
     v[j] = x;
+    key[j] = in ? float_key(x) : 0u;
   }
-  float mx = -INFINITY;
+  // K = the k-th largest key: the largest K with #(key >= K) >= k.
+  uint32_t K = 0;
+#pragma unroll 1
+  for (int b = 31; b >= 0; --b) {
+    const uint32_t cand = K | (1u << b);
+    int cnt = 0;
 #pragma unroll
-  for (int j = 0; j < kMaxExpertsPerLane; ++j) mx = fmaxf(mx, v[j]);
-  mx = wave_max(mx);
-  float denom_all = 0.0f;
-  if (!renorm) {
+    for (int j = 0; j < kMaxExpertsPerLane; ++j)
+      if (j < per) cnt += __popcll(__ballot(key[j] >= cand));
+    if (cnt >= k) K = cand;
+  }
+  int above = 0;
+#pragma unroll
+  for (int j = 0; j < kMaxExpertsPerLane; ++j)
+    if (j < per) above += __popcll(__ballot(key[j] > K));
+  // Selected: every key above K, then the first (k - above) keys equal to K
+  // in expert order; compacted into LDS in expert order.
+  int ties_before = 0, sel_before = 0;
+#pragma unroll
+  for (int j = 0; j < kMaxExpertsPerLane; ++j) {
+    if (j < per) {
+      const uint64_t tie = __ballot(key[j] == K && key[j] != 0u);
+      const bool is_tie = (tie >> lane) & 1ull;
+      const int tie_rank = ties_before + __popcll(tie & lt);
+      const bool sel = key[j] > K || (is_tie && tie_rank < k - above);
+      const uint64_t selm = __ballot(sel);
+      if (sel) {
+        const int pos = sel_before + __popcll(selm & lt);
+        sc.key[pos] = key[j];
+        sc.id[pos] = lane + 64 * j;
+        sc.val[pos] = v[j];
+      }
+      ties_before += __popcll(tie);
+      sel_before += __popcll(selm);
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  uint32_t mk = 0;
+  int mid = 0;
+  float mv = 0.0f;
+  int rank = 0;
+  if (lane < k) {
+    mk = sc.key[lane];
+    mid = sc.id[lane];
+    mv = sc.val[lane];
+    for (int q = 0; q < k; ++q) {
+      const uint32_t kq = sc.key[q];
+      rank += (kq > mk) || (kq == mk && sc.id[q] < mid);
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  if (lane < k) {
+    sc.id[rank] = mid;
+    sc.val[rank] = mv;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  const float mx = sc.val[0];
+  my_id = lane < k ? sc.id[lane] : 0;
+  const float my_v = lane < k ? sc.val[lane] : -INFINITY;
+  const float my_e = lane < k ? __expf(my_v - mx) : 0.0f;
+  float denom;
+  if (renorm) {
+    denom = wave_sum(my_e);
+  } else {
     float s = 0.0f;
 #pragma unroll
     for (int j = 0; j < kMaxExpertsPerLane; ++j)
       if (j < per && lane + 64 * j < E) s += __expf(v[j] - mx);
-    denom_all = wave_sum(s);
+    denom = wave_sum(s);
   }
-  uint32_t taken = 0;  // bit j: element j of this lane already selected
-  float sel_sum = 0.0f;
-  float my_e = 0.0f;   // lane r keeps exp(sel_r - mx)
-  my_id = 0;
-  for (int r = 0; r < k; ++r) {
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
-#pragma unroll
-    for (int j = 0; j < kMaxExpertsPerLane; ++j) {
-      const int e = lane + 64 * j;
-      if (j < per && e < E && !((taken >> j) & 1u)) {
-        if (v[j] > bv || (v[j] == bv && e < bi)) { bv = v[j]; bi = e; }
-      }
-    }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-      const float ov = __shfl_xor(bv, o, kWave);
-      const int oi = __shfl_xor(bi, o, kWave);
-      if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-    }
-    if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
-    const float ev = __expf(bv - mx);
-    sel_sum += ev;
-    if (lane == r) { my_e = ev; my_id = bi; }
-  }
-  return renorm ? my_e / sel_sum : my_e / denom_all;
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();  // the scratch is reused by the wave's next token
+  return my_e / denom;
 }
 
 // One wave per token.
-template <bool BF16_LOGITS>
+template <bool BF16_LOGITS, int PER>
 __global__ void __launch_bounds__(256)
     route_topk_kernel(const void* __restrict__ logits, int64_t ldl, int T, int E, int k, int renorm,
                       int32_t* __restrict__ ids, float* __restrict__ wts, int64_t ldo) {
+  __shared__ RouteScratch scratch[4];
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
   int my_id = 0;
-  const float w = route_token<BF16_LOGITS>(logits, ldl, t, E, k, renorm, my_id);
+  const float w = route_token<BF16_LOGITS, PER>(logits, ldl, t, E, k, renorm, my_id, scratch[threadIdx.x >> 6]);
   if (lane < k) {
     ids[(int64_t)t * ldo + lane] = my_id;
     wts[(int64_t)t * ldo + lane] = w;
@@ -162,12 +230,20 @@ __device__ void align_block(const int32_t* ids, int S, int E, int block_m, int32
     }
     expert_ids[b] = ex;
   }
-  // Stable scatter: rank = earlier slots of the same expert.
+  // Stable scatter: rank = earlier slots of the same expert, counted four
+  // ids per LDS read with independent reads in flight.
   if (tid < S) {
     const int e = ids[tid];
     if (e >= 0 && e < E) {
       int rank = 0;
-      for (int j = 0; j < tid; ++j) rank += (ids[j] == e);
+      const int4* v4 = reinterpret_cast<const int4*>(ids);
+      const int n4 = tid >> 2;
+#pragma unroll 8
+      for (int j = 0; j < n4; ++j) {
+        const int4 q = v4[j];
+        rank += (q.x == e) + (q.y == e) + (q.z == e) + (q.w == e);
+      }
+      for (int j = n4 * 4; j < tid; ++j) rank += (ids[j] == e);
       sorted_ids[off[e] + rank] = tid;
     }
   }
@@ -177,7 +253,7 @@ __global__ void __launch_bounds__(1024)
     align_small_kernel(const int32_t* __restrict__ topk_ids, int S, int E, int block_m,
                        int32_t* __restrict__ sorted_ids, int64_t sorted_cap, int32_t* __restrict__ expert_ids,
                        int64_t blocks_cap, int32_t* __restrict__ num_post) {
-  __shared__ int32_t ids[kAlignSmall];
+  __shared__ __align__(16) int32_t ids[kAlignSmall];
   __shared__ int cnt[1024], off[1024], wave_tot[16];
   if ((int)threadIdx.x < S) ids[threadIdx.x] = topk_ids[threadIdx.x];
   __syncthreads();
@@ -186,18 +262,19 @@ __global__ void __launch_bounds__(1024)
 
 // Router and align in one block: 16 waves route the T tokens (T * k <= 1024),
 // then the block aligns the slot ids it just produced.
-template <bool BF16_LOGITS>
+template <bool BF16_LOGITS, int PER>
 __global__ void __launch_bounds__(1024)
     route_align_small_kernel(const void* __restrict__ logits, int64_t ldl, int T, int E, int k, int renorm,
                              int32_t* __restrict__ topk_ids, float* __restrict__ topk_w, int block_m,
                              int32_t* __restrict__ sorted_ids, int64_t sorted_cap, int32_t* __restrict__ expert_ids,
                              int64_t blocks_cap, int32_t* __restrict__ num_post) {
-  __shared__ int32_t ids[kAlignSmall];
+  __shared__ __align__(16) int32_t ids[kAlignSmall];
   __shared__ int cnt[1024], off[1024], wave_tot[16];
+  __shared__ RouteScratch scratch[16];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   for (int t = wave; t < T; t += 16) {
     int my_id = 0;
-    const float w = route_token<BF16_LOGITS>(logits, ldl, t, E, k, renorm, my_id);
+    const float w = route_token<BF16_LOGITS, PER>(logits, ldl, t, E, k, renorm, my_id, scratch[wave]);
     if (lane < k) {
       ids[t * k + lane] = my_id;
       topk_ids[(int64_t)t * k + lane] = my_id;
@@ -346,6 +423,20 @@ __global__ void __launch_bounds__(256)
   *reinterpret_cast<u32x4*>(out + t * ldo + h) = o;
 }
 
+// Logits per lane for E experts (the router's unroll), and the logits type.
+template <class F>
+void per_dispatch(int64_t E, bool bf16, F&& go) {
+  auto with = [&](auto per_tag) {
+    if (bf16) go(std::true_type{}, per_tag);
+    else go(std::false_type{}, per_tag);
+  };
+  if (E <= 64) with(std::integral_constant<int, 1>{});
+  else if (E <= 128) with(std::integral_constant<int, 2>{});
+  else if (E <= 256) with(std::integral_constant<int, 4>{});
+  else if (E <= 512) with(std::integral_constant<int, 8>{});
+  else with(std::integral_constant<int, kMaxExpertsPerLane>{});
+}
+
 }  // namespace
 }  // namespace strix
 
@@ -366,12 +457,13 @@ int strix_moe_route_topk(const void* logits, int logits_dtype, int64_t ldl, int6
   if (T == 0) return STRIX_OK;
   STRIX_ARCH_GATE();
   const unsigned blocks = (unsigned)((T + 3) / 4);
-  if (logits_dtype == STRIX_BF16)
-    hipLaunchKernelGGL(route_topk_kernel<true>, dim3(blocks), dim3(256), 0, as_stream(stream), logits, ldl,
+  auto go = [&](auto bf16_tag, auto per_tag) {
+    constexpr bool BF = decltype(bf16_tag)::value;
+    constexpr int PER = decltype(per_tag)::value;
+    hipLaunchKernelGGL((route_topk_kernel<BF, PER>), dim3(blocks), dim3(256), 0, as_stream(stream), logits, ldl,
                        (int)T, (int)E, (int)top_k, renormalize, topk_ids, topk_weights, ldo);
-  else
-    hipLaunchKernelGGL(route_topk_kernel<false>, dim3(blocks), dim3(256), 0, as_stream(stream), logits, ldl,
-                       (int)T, (int)E, (int)top_k, renormalize, topk_ids, topk_weights, ldo);
+  };
+  per_dispatch(E, logits_dtype == STRIX_BF16, go);
   return check_launch(op);
 }
 
@@ -424,7 +516,9 @@ int strix_moe_route_align(const void* logits, int logits_dtype, int64_t ldl, int
                           int32_t* sorted_ids, int64_t sorted_cap, int32_t* expert_ids, int64_t blocks_cap,
                           int32_t* num_post, void* workspace, int64_t workspace_bytes, void* stream) {
   const char* op = "moe_route_align";
-  if (T * top_k > kAlignSmall || T == 0) {
+  // One block routes at most one token per wave (16 tokens) before the
+  // separate, grid-wide router is faster.
+  if (T * top_k > kAlignSmall || T > 16 || T == 0) {
     int rc = strix_moe_route_topk(logits, logits_dtype, ldl, T, E, top_k, renormalize, topk_ids, topk_weights, top_k,
                                   stream);
     if (rc) return rc;
@@ -441,14 +535,14 @@ int strix_moe_route_align(const void* logits, int logits_dtype, int64_t ldl, int
   STRIX_REQUIRE(sorted_cap >= strix_moe_align_sorted_capacity(T * top_k, E, block_m), "%s: sorted_ids too small", op);
   STRIX_REQUIRE(blocks_cap * block_m >= sorted_cap, "%s: expert_ids needs ceil(capacity / block_m) entries", op);
   STRIX_ARCH_GATE();
-  if (logits_dtype == STRIX_BF16)
-    hipLaunchKernelGGL(route_align_small_kernel<true>, dim3(1), dim3(1024), 0, as_stream(stream), logits, ldl, (int)T,
-                       (int)E, (int)top_k, renormalize, topk_ids, topk_weights, (int)block_m, sorted_ids, sorted_cap,
-                       expert_ids, blocks_cap, num_post);
-  else
-    hipLaunchKernelGGL(route_align_small_kernel<false>, dim3(1), dim3(1024), 0, as_stream(stream), logits, ldl,
+  auto go = [&](auto bf16_tag, auto per_tag) {
+    constexpr bool BF = decltype(bf16_tag)::value;
+    constexpr int PER = decltype(per_tag)::value;
+    hipLaunchKernelGGL((route_align_small_kernel<BF, PER>), dim3(1), dim3(1024), 0, as_stream(stream), logits, ldl,
                        (int)T, (int)E, (int)top_k, renormalize, topk_ids, topk_weights, (int)block_m, sorted_ids,
                        sorted_cap, expert_ids, blocks_cap, num_post);
+  };
+  per_dispatch(E, logits_dtype == STRIX_BF16, go);
   return check_launch(op);
 }
 

@@ -197,14 +197,15 @@ KERNELS: list[Kernel] = [
     Kernel(
         "moe_route_align",
         "moe_route_align_small",
-        "router top-k and align in one 1024-thread block launch (T * top_k <= 1024); the same outputs "
-        "as moe_route_topk then moe_align",
-        {"logits_dtype": ("fp32", "bf16"), "num_experts": Range(hi=1024), "num_slots": Range(hi=1024)},
+        "router top-k and align in one 1024-thread block launch (T <= 16, T * top_k <= 1024); the same "
+        "outputs as moe_route_topk then moe_align",
+        {"logits_dtype": ("fp32", "bf16"), "num_experts": Range(hi=1024), "tokens": Range(lo=1, hi=16),
+         "num_slots": Range(hi=1024)},
     ),
     Kernel(
         "moe_route_align",
         "moe_route_then_align",
-        "moe_route_topk then the three-pass moe_align (more than 1024 slots)",
+        "moe_route_topk (one wave per token, grid-wide) then moe_align",
         {"logits_dtype": ("fp32", "bf16"), "num_experts": Range(hi=1024)},
     ),
     Kernel(

@@ -359,8 +359,9 @@ def _(topk_ids, num_experts, block_m):
     return (topk_ids.new_empty((cap,)), topk_ids.new_empty((nblk,)), topk_ids.new_empty((1,)))
 
 
-# Extension: the router and the align as one op (T * top_k <= 1024 runs as
-# one single-block kernel); same outputs as moe_route_topk then moe_align.
+# Extension: the router and the align as one op (up to 16 tokens and 1024
+# slots it runs as one single-block kernel); same outputs as moe_route_topk
+# then moe_align.
 @_define("moe_route_align(Tensor logits, int top_k, int block_m, bool renormalize=True) "
          "-> (Tensor, Tensor, Tensor, Tensor, Tensor)")
 def moe_route_align(logits, top_k, block_m, renormalize=True):
