@@ -355,8 +355,14 @@ __global__ void __launch_bounds__(256) stream8_kernel(G8 p) {
 // reads are conflict-free. R-1 slots are in flight while one is consumed and
 // in-flight data costs no registers. Whole-line copies stream from HBM
 // markedly faster than the 16-row x 64-byte pattern of register fragments.
-template <int KIND, int NT, bool MOE, int EPI, int ACT, int R, bool WX128, int TQ, int NW>
-__global__ void __launch_bounds__(64 * NW) ring8_kernel(G8 p) {
+//
+// KS > 1 (with NW == 1): KS waves of the block split K, each with its own
+// ring over a contiguous range of 128-K steps, and add their partial sums
+// through LDS at the end. It multiplies the waves, and so the bytes in
+// flight per CU, when the output columns alone leave few waves per CU
+// (decode on short N, MoE decode over a few experts).
+template <int KIND, int NT, bool MOE, int EPI, int ACT, int R, bool WX128, int TQ, int NW, int KS = 1>
+__global__ void __launch_bounds__(64 * NW * KS) ring8_kernel(G8 p) {
   constexpr bool GATED = (EPI == kEpiGated);
   constexpr int NTH = GATED ? NT / 2 : NT;
   constexpr bool INT_ACC = (KIND == kI8Token);
@@ -368,15 +374,19 @@ __global__ void __launch_bounds__(64 * NW) ring8_kernel(G8 p) {
   constexpr int WQ = 2 * NT;                        // weight copies per wave and slot
   constexpr int EX = TQ + (SCALES ? 1 : 0);         // shared copies per slot
   static_assert(NW == 1 || EX <= NW, "one shared copy per wave at most");
+  static_assert(KS == 1 || NW == 1, "K split and shared token copies do not combine");
   constexpr int E_HI = NW == 1 ? EX : 1;            // shared copies of a wave that has any
   constexpr int TOK_OFF = NW * NT * 2048;
-  constexpr int SC_OFF = TOK_OFF + 2048;
+  constexpr int SC_OFF = TOK_OFF + TQ * 1024;
   constexpr int SLOT = SC_OFF + (SCALES ? 256 : 0);
   static_assert((R - 2) * (WQ + E_HI) < 64, "vmcnt counts at most 63 copies");
-  __shared__ __attribute__((aligned(1024))) uint8_t ring[R * SLOT];
+  static_assert(KS == 1 || R * SLOT >= NT * 4 * 64 * 4, "a wave's ring holds its partial sums");
+  __shared__ __attribute__((aligned(1024))) uint8_t ring_all[KS * R * SLOT];
 
   const int lane = threadIdx.x & 63;
   const int wave = NW == 1 ? 0 : __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int kw = KS == 1 ? 0 : __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // K-split wave
+  uint8_t* ring = ring_all + kw * (R * SLOT);
   const int r16 = lane & 15, g4 = lane >> 4;
   const int m0 = blockIdx.y * 16;
   int expert = 0;
@@ -472,12 +482,14 @@ __global__ void __launch_bounds__(64 * NW) ring8_kernel(G8 p) {
     acci[s] = v4i{0, 0, 0, 0};
   }
 
-  const int nks = p.K >> 7;
+  const int nks_all = p.K >> 7;
+  const int kb0 = KS == 1 ? 0 : kw * nks_all / KS;
+  const int nks = KS == 1 ? nks_all : (kw + 1) * nks_all / KS;  // this wave's steps end here
 #pragma unroll
   for (int s0 = 0; s0 < R - 1; ++s0)
-    if (s0 < nks) issue(s0, s0);
+    if (kb0 + s0 < nks) issue(kb0 + s0, s0);
   int slot = 0;
-  for (int kb = 0; kb < nks; ++kb) {
+  for (int kb = kb0; kb < nks; ++kb) {
     constexpr int AHEAD = R - 2;  // slots issued after slot kb, in steady state
     if (kb + AHEAD <= nks - 1) {
       if (ne == E_HI) wait_vmcnt<AHEAD * (WQ + E_HI)>(); else wait_vmcnt<AHEAD * WQ>();
@@ -526,6 +538,31 @@ __global__ void __launch_bounds__(64 * NW) ring8_kernel(G8 p) {
       }
     }
     slot = slot == R - 1 ? 0 : slot + 1;
+  }
+
+  if constexpr (KS > 1) {
+    // Partial sums through each wave's own (drained) ring; wave 0 adds them.
+    wait_vmcnt<0>();
+    float* red = reinterpret_cast<float*>(ring);
+#pragma unroll
+    for (int s2 = 0; s2 < NT; ++s2)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        red[(s2 * 4 + i) * 64 + lane] = INT_ACC ? __int_as_float(acci[s2][i]) : acc[s2][i];
+    __syncthreads();
+    if (kw != 0) return;
+#pragma unroll
+    for (int w = 1; w < KS; ++w) {
+      const float* rw = reinterpret_cast<const float*>(ring_all + w * (R * SLOT));
+#pragma unroll
+      for (int s2 = 0; s2 < NT; ++s2)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float v = rw[(s2 * 4 + i) * 64 + lane];
+          if constexpr (INT_ACC) acci[s2][i] += __float_as_int(v);
+          else acc[s2][i] += v;
+        }
+    }
   }
 
   if (nout0 >= p.n_out) return;
@@ -862,17 +899,48 @@ int launch_stream(const G8& p, int grid_y, hipStream_t st, const char* op) {
   return check_launch(op);
 }
 
-template <int KIND, int NT, bool MOE, int EPI, int ACT, int R, bool WX128, int NW>
+// K-split factor of the ring kernel. Below four output waves per CU, four
+// waves split K (two if K is too short for four steps each); from four per
+// CU up a split only adds ring fills and a reduction (measured on MI355X:
+// INT8 N=K=5120 at M=1 9.1 -> 7.6 us with the split, FP8 N=17408 K=5120 at
+// M=1 20.2 -> 22.1 us with a two-way split). MoE blocks past the routed
+// slots exit at once, so they do not count as waves.
+inline int ring_ksplit(const G8& p, int64_t waves) {
+  const int nks = p.K >> 7;
+  if (waves >= 4LL * cu_count()) return 1;
+  if (nks >= 16) return 4;
+  if (nks >= 8) return 2;
+  return 1;
+}
+
+template <int KIND, int NT, bool MOE, int EPI, int ACT, int R, bool WX128, int NW, bool SPLIT = false>
 int launch_ring(const G8& p, int grid_y, hipStream_t st, const char* op) {
   constexpr int NTH = (EPI == kEpiGated) ? NT / 2 : NT;
   const int groups = (p.n_out + 16 * NTH - 1) / (16 * NTH);
   const int grid_x = (groups + NW - 1) / NW;
-  if (!MOE && p.M <= 8)
-    hipLaunchKernelGGL((ring8_kernel<KIND, NT, MOE, EPI, ACT, R, WX128, 1, NW>), dim3(grid_x, grid_y), dim3(64 * NW),
-                       0, st, p);
-  else
-    hipLaunchKernelGGL((ring8_kernel<KIND, NT, MOE, EPI, ACT, R, WX128, 2, NW>), dim3(grid_x, grid_y), dim3(64 * NW),
-                       0, st, p);
+  const bool tq1 = !MOE && p.M <= 8;
+  int ks = 1;
+  if constexpr (SPLIT && NW == 1) {
+    const int64_t live_y = MOE ? std::min<int64_t>(grid_y, p.num_slots) : grid_y;
+    ks = ring_ksplit(p, (int64_t)grid_x * live_y);
+  }
+  auto go = [&](auto tq_tag, auto ks_tag) {
+    constexpr int TQ_ = decltype(tq_tag)::value;
+    constexpr int KS_ = decltype(ks_tag)::value;
+    hipLaunchKernelGGL((ring8_kernel<KIND, NT, MOE, EPI, ACT, R, WX128, TQ_, NW, KS_>), dim3(grid_x, grid_y),
+                       dim3(64 * NW * KS_), 0, st, p);
+  };
+  auto with_tq = [&](auto ks_tag) {
+    if (tq1) go(std::integral_constant<int, 1>{}, ks_tag);
+    else go(std::integral_constant<int, 2>{}, ks_tag);
+  };
+  if constexpr (SPLIT && NW == 1) {
+    if (ks == 4) with_tq(std::integral_constant<int, 4>{});
+    else if (ks == 2) with_tq(std::integral_constant<int, 2>{});
+    else with_tq(std::integral_constant<int, 1>{});
+  } else {
+    with_tq(std::integral_constant<int, 1>{});
+  }
   return check_launch(op);
 }
 
@@ -944,7 +1012,7 @@ int dense_dispatch(const G8& p, hipStream_t st, const char* op, int cfg) {
     else cfg = 6;
   }
   switch (cfg) {
-    case 0: return launch_ring<KIND, 1, false, EPI, kActSilu, 5, WX128, 1>(p, (M + 15) / 16, st, op);
+    case 0: return launch_ring<KIND, 1, false, EPI, kActSilu, 5, WX128, 1, true>(p, (M + 15) / 16, st, op);
     case 1: return launch_stream<KIND, 1, 2, 4, false, EPI, kActSilu, 4, WX128>(p, (M + 31) / 32, st, op);
     case 2: return launch_stream<KIND, 1, 4, 4, false, EPI, kActSilu, 2, WX128>(p, (M + 63) / 64, st, op);
     case 3: return launch_tiled<KIND, 128, 128, 2, 2, 4, false, EPI, kActSilu, WX128>(p, 0, st, op);
@@ -969,7 +1037,7 @@ template <int KIND, int EPI, int ACT>
 int moe_dispatch(const G8& p, int block_m, int num_blocks, hipStream_t st, const char* op) {
   constexpr int NTS = (EPI == kEpiGated) ? 2 : 1;
   switch (block_m) {
-    case 16: return launch_ring<KIND, NTS, true, EPI, ACT, 5, false, 1>(p, num_blocks, st, op);
+    case 16: return launch_ring<KIND, NTS, true, EPI, ACT, 5, false, 1, true>(p, num_blocks, st, op);
     case 32: return launch_stream<KIND, NTS, 2, 2, true, EPI, ACT, 4, false>(p, num_blocks, st, op);
     case 64: return launch_tiled<KIND, 64, 128, 1, 4, 4, true, EPI, ACT, false>(p, num_blocks, st, op);
     case 128: return launch_tiled<KIND, 128, 128, 2, 2, 4, true, EPI, ACT, false>(p, num_blocks, st, op);

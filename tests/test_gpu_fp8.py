@@ -38,7 +38,7 @@ def test_config2_sweep(m, c2_weights):
 
 
 @pytest.mark.parametrize("m", [1, 6, 16, 17, 33, 64, 65, 129, 300])
-@pytest.mark.parametrize("n,k", [(300, 1024), (1024, 2048)])
+@pytest.mark.parametrize("n,k", [(300, 1024), (1024, 2048), (520, 4096)])
 def test_shapes_and_ragged_n(m, n, k):
     d = workloads.c2_fp8(seed=m, m=m, n=n, k=k)
     qa, sa = oracle.fp8_quant_group128(d["x"])

@@ -43,8 +43,10 @@ def test_config1_bf16_output():
 
 
 @pytest.mark.parametrize("m", [1, 5, 16, 17, 33, 64, 100, 300])
-@pytest.mark.parametrize("n,k", [(384, 1024), (200, 2048)])
+@pytest.mark.parametrize("n,k", [(384, 1024), (200, 2048), (520, 4096)])
 def test_accumulator_shapes(m, n, k):
+    """K 2048 and 4096 at M <= 32 run the decode ring split over 2 and 4
+    waves of K: the int32 partial sums must still add up exactly."""
     d, q, s = _case(m, n, k, seed=m)
     acc = torch.ops.strix._w8a8_i32_acc(q.to(DEV), d["w"].to(DEV)).cpu().numpy()
     assert np.array_equal(acc, oracle.w8a8_int8_acc(q, d["w"]))
