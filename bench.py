@@ -45,7 +45,7 @@ class Timer:
     def __init__(self, torch):
         self.torch = torch
 
-    def __call__(self, fn, iters: int, warmup: int = 2) -> float:
+    def __call__(self, fn, iters: int, warmup: int = 10) -> float:
         torch = self.torch
         for _ in range(warmup):
             fn(0)

@@ -34,18 +34,13 @@ from libstrix_amd.vllm_plugin import disabled, model_gate
 # The sorted-id block (block_m) picks the kernel family: 16 streams the
 # experts' weights through a per-wave LDS ring (decode), 32 a register-pipelined
 # stream, 64/128/256 the LDS-tiled MFMA kernels. It is chosen from the mean
-# rows per expert, tokens * top_k / E, so one table serves every model shape
-# (the reference keys per-model tables on the token count alone,
-# python/strix_vllm/moe.py:40-138).
-_BM_STEPS = ((16, 16), (32, 32), (96, 64))
-
-
+# rows per expert, tokens * top_k / E (functional.moe_block_m), so one table
+# serves every model shape (the reference keys per-model tables on the token
+# count alone, python/strix_vllm/moe.py:40-138).
 def _block_m(num_tokens: int, top_k: int, num_experts: int) -> int:
-    per_expert = num_tokens * top_k / max(num_experts, 1)
-    for limit, bm in _BM_STEPS:
-        if per_expert <= limit:
-            return bm
-    return 128
+    from libstrix_amd.functional import moe_block_m
+
+    return moe_block_m(num_tokens, top_k, num_experts)
 
 
 def _block_n(*ns: int) -> int:

@@ -117,16 +117,17 @@ def test_register_needs_vllm(clean_env, monkeypatch):
 
 # ------------------------------------------------------------------ tile tables and gates
 def test_block_m_by_rows_per_expert():
-    # config 3 (E=128, top-8): decode rides the 16-row ring, prefill the 128 tile
+    # config 3 (E=128, top-8): decode rides the 16-row ring, prefill the 256 tile
     assert moe.fp8_blocks(1) == (16, 128)
     assert moe.fp8_blocks(64)[0] == 16
-    assert moe.fp8_blocks(4096)[0] == 128
+    assert moe.fp8_blocks(4096)[0] == 256
+    assert moe.fp8_blocks(1024)[0] == 128
     # config 4 (E=32, top-4): 2048 tokens = 256 rows per expert
-    assert moe.strix_blocks(2048, 4, 32) == (128, 64)
+    assert moe.strix_blocks(2048, 4, 32) == (256, 64)
     prev = 0
-    for t in (1, 2, 8, 64, 128, 512, 1024, 4096, 65536):
+    for t in (1, 2, 8, 64, 128, 512, 700, 1024, 4096, 65536):
         bm = moe.strix_blocks(t, 8, 128)[0]
-        assert bm in (16, 32, 64, 128) and bm >= prev
+        assert bm in (16, 32, 64, 128, 256) and bm >= prev
         prev = bm
     assert moe.wna16_blocks(8192, 1536, 2048) == moe.strix_blocks(8192)
     assert moe.fp8_raw_blocks(300) == moe.strix_blocks(300)
