@@ -903,13 +903,22 @@ int launch_stream(const G8& p, int grid_y, hipStream_t st, const char* op) {
 // waves split K (two if K is too short for four steps each); from four per
 // CU up a split only adds ring fills and a reduction (measured on MI355X:
 // INT8 N=K=5120 at M=1 9.1 -> 7.6 us with the split, FP8 N=17408 K=5120 at
-// M=1 20.2 -> 22.1 us with a two-way split). MoE blocks past the routed
-// slots exit at once, so they do not count as waves.
-inline int ring_ksplit(const G8& p, int64_t waves) {
+// M=1 20.2 -> 22.1 us with a two-way split).
+//
+// With one token copy per step (M <= 8) the split is taken while every block
+// stays resident in one round (160 KiB of LDS per CU). With two token copies
+// (M 9..32) it pays only on short K (measured: INT8 N=K=5120 at M=32 10.9 ->
+// 10.1 us with four waves; FP8 N=5120 K=17408 at M=16 28 -> 32-36 us with two
+// or four), so there it needs K <= 8192.
+inline int ring_ksplit(const G8& p, int64_t waves, int64_t blocks, int64_t ring_bytes, bool tq1) {
   const int nks = p.K >> 7;
-  if (waves >= 4LL * cu_count()) return 1;
-  if (nks >= 16) return 4;
-  if (nks >= 8) return 2;
+  const int64_t cus = cu_count();
+  if (waves >= 4 * cus) return 1;
+  const int top = nks >= 16 ? 4 : nks >= 8 ? 2 : 1;
+  if (!tq1) return nks <= 64 ? top : 1;
+  const int64_t per_cu = (blocks + cus - 1) / cus;
+  for (int ks = top; ks > 1; ks /= 2)
+    if (per_cu * ks * ring_bytes <= 160 * 1024) return ks;
   return 1;
 }
 
@@ -921,8 +930,10 @@ int launch_ring(const G8& p, int grid_y, hipStream_t st, const char* op) {
   const bool tq1 = !MOE && p.M <= 8;
   int ks = 1;
   if constexpr (SPLIT && NW == 1) {
-    const int64_t live_y = MOE ? std::min<int64_t>(grid_y, p.num_slots) : grid_y;
-    ks = ring_ksplit(p, (int64_t)grid_x * live_y);
+    constexpr bool SCALES = (KIND != kI8Token);
+    const int64_t tq = tq1 ? 1 : 2;
+    const int64_t ring_bytes = (int64_t)R * (NT * 2048 + tq * 1024 + (SCALES ? 256 : 0));
+    ks = ring_ksplit(p, (int64_t)grid_x * grid_y, (int64_t)grid_x * grid_y, ring_bytes, tq1);
   }
   auto go = [&](auto tq_tag, auto ks_tag) {
     constexpr int TQ_ = decltype(tq_tag)::value;
@@ -1037,7 +1048,8 @@ template <int KIND, int EPI, int ACT>
 int moe_dispatch(const G8& p, int block_m, int num_blocks, hipStream_t st, const char* op) {
   constexpr int NTS = (EPI == kEpiGated) ? 2 : 1;
   switch (block_m) {
-    case 16: return launch_ring<KIND, NTS, true, EPI, ACT, 5, false, 1, true>(p, num_blocks, st, op);
+    // No K split here: measured slower at T=1 (29 -> 32 us for config 3).
+    case 16: return launch_ring<KIND, NTS, true, EPI, ACT, 5, false, 1>(p, num_blocks, st, op);
     case 32: return launch_stream<KIND, NTS, 2, 2, true, EPI, ACT, 4, false>(p, num_blocks, st, op);
     case 64: return launch_tiled<KIND, 64, 128, 1, 4, 4, true, EPI, ACT, false>(p, num_blocks, st, op);
     case 128: return launch_tiled<KIND, 128, 128, 2, 2, 4, true, EPI, ACT, false>(p, num_blocks, st, op);
