@@ -368,8 +368,13 @@ __global__ void __launch_bounds__(64 * NW * KS) ring8_kernel(G8 p) {
   constexpr bool INT_ACC = (KIND == kI8Token);
   constexpr bool SCALES = (KIND != kI8Token);
   // TQ token copies of 8 rows per slot: 1 when the block has at most 8 token
-  // rows (lanes of the missing rows read row 0), else 2.
-  static_assert(TQ == 1 || TQ == 2, "one or two 8-row token copies");
+  // rows (lanes of the missing rows read row 0), 2 for 16 rows, 4 for 32
+  // rows (two token subtiles per wave, so the weights stream once up to 32
+  // rows).
+  static_assert(TQ == 1 || TQ == 2 || TQ == 4, "one, two or four 8-row token copies");
+  static_assert(TQ < 4 || (!MOE && NW == 1), "32 token rows: dense, one wave per block");
+  constexpr int MT = TQ == 4 ? 2 : 1;               // 16-token subtiles per wave
+  constexpr int SAL = 16 * MT;                      // scale lanes of the token rows
   static_assert(NW == 1 || KIND != kI8Group, "int8 group weight scales need one lane per weight row");
   constexpr int WQ = 2 * NT;                        // weight copies per wave and slot
   constexpr int EX = TQ + (SCALES ? 1 : 0);         // shared copies per slot
@@ -380,7 +385,7 @@ __global__ void __launch_bounds__(64 * NW * KS) ring8_kernel(G8 p) {
   constexpr int SC_OFF = TOK_OFF + TQ * 1024;
   constexpr int SLOT = SC_OFF + (SCALES ? 256 : 0);
   static_assert((R - 2) * (WQ + E_HI) < 64, "vmcnt counts at most 63 copies");
-  static_assert(KS == 1 || R * SLOT >= NT * 4 * 64 * 4, "a wave's ring holds its partial sums");
+  static_assert(KS == 1 || R * SLOT >= NT * MT * 4 * 64 * 4, "a wave's ring holds its partial sums");
   __shared__ __attribute__((aligned(1024))) uint8_t ring_all[KS * R * SLOT];
 
   const int lane = threadIdx.x & 63;
@@ -388,7 +393,7 @@ __global__ void __launch_bounds__(64 * NW * KS) ring8_kernel(G8 p) {
   const int kw = KS == 1 ? 0 : __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // K-split wave
   uint8_t* ring = ring_all + kw * (R * SLOT);
   const int r16 = lane & 15, g4 = lane >> 4;
-  const int m0 = blockIdx.y * 16;
+  const int m0 = blockIdx.y * 16 * MT;
   int expert = 0;
   if constexpr (MOE) {
     if (m0 >= *p.num_post) return;
@@ -430,14 +435,15 @@ __global__ void __launch_bounds__(64 * NW * KS) ring8_kernel(G8 p) {
     token_row<MOE>(p, m0 + row, br, orw, v);
     tsrc[e] = p.a + (int64_t)br * p.lda + 16 * ((lane & 7) ^ lds_swz(row));
   }
-  // Scale copy: lanes 0..15 the token rows' activation scales, lanes 16.. the
-  // weight scales (fp8: one per subtile of the block; int8 group: one per row).
+  // Scale copy: lanes 0..SAL-1 the token rows' activation scales, lanes
+  // SAL.. the weight scales (fp8: one per subtile of the block; int8 group:
+  // one per row).
   const float* ssrc = nullptr;
   int64_t sstride = 0;
   if constexpr (SCALES) {
     int br, orw;
     bool v;
-    if (lane < 16) {
+    if (lane < SAL) {
       token_row<MOE>(p, m0 + lane, br, orw, v);
       ssrc = p.sa + (int64_t)br * p.sa_rs;
       sstride = p.sa_ks;
@@ -445,13 +451,13 @@ __global__ void __launch_bounds__(64 * NW * KS) ring8_kernel(G8 p) {
       const float* swb = p.sw + (int64_t)expert * p.sw_es;
       int wr;
       if constexpr (KIND == kFp8Block) {
-        const int j = min(lane - 16, NW * NT - 1);  // subtile j of the block
+        const int j = min(lane - SAL, NW * NT - 1);  // subtile j of the block
         const int jw = j / NT, js = j % NT;           // its wave and slot
         const int n0 = (blockIdx.x * NW + jw) * (16 * NTH);
         const int r0 = GATED ? (js < NTH ? n0 + 16 * js : p.gate_off + n0 + 16 * (js - NTH)) : n0 + 16 * js;
         wr = min(r0, p.N - 1) >> 7;
       } else {
-        const int j = min(lane - 16, 16 * NT - 1);
+        const int j = min(lane - SAL, 16 * NT - 1);
         wr = min(wrow0[j >> 4] + (j & 15), p.N - 1);
       }
       ssrc = swb + (int64_t)wr * p.sw_ns;
@@ -474,13 +480,15 @@ __global__ void __launch_bounds__(64 * NW * KS) ring8_kernel(G8 p) {
   const int tr = (TQ == 1 && r16 >= 8) ? 0 : r16;  // token row this lane reads
   const uint32_t tfrag0 = (uint32_t)tr * 128 + 16 * (g4 ^ lds_swz(tr));
   const uint32_t tfrag1 = (uint32_t)tr * 128 + 16 * ((4 + g4) ^ lds_swz(tr));
-  v4f acc[NT];
-  v4i acci[NT];
+  v4f acc[NT][MT];
+  v4i acci[NT][MT];
 #pragma unroll
-  for (int s = 0; s < NT; ++s) {
-    acc[s] = v4f{0.f, 0.f, 0.f, 0.f};
-    acci[s] = v4i{0, 0, 0, 0};
-  }
+  for (int s = 0; s < NT; ++s)
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      acc[s][t] = v4f{0.f, 0.f, 0.f, 0.f};
+      acci[s][t] = v4i{0, 0, 0, 0};
+    }
 
   const int nks_all = p.K >> 7;
   const int kb0 = KS == 1 ? 0 : kw * nks_all / KS;
@@ -498,7 +506,10 @@ __global__ void __launch_bounds__(64 * NW * KS) ring8_kernel(G8 p) {
     }
     if constexpr (NW > 1) lds_barrier();  // shared token and scale copies of other waves
     const uint8_t* st = ring + slot * SLOT;
-    const v8i bf = cat8(lds128(st + TOK_OFF + tfrag0), lds128(st + TOK_OFF + tfrag1));
+    v8i bf[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+      bf[t] = cat8(lds128(st + TOK_OFF + t * 2048 + tfrag0), lds128(st + TOK_OFF + t * 2048 + tfrag1));
     v8i af[NT];
 #pragma unroll
     for (int s = 0; s < NT; ++s) {
@@ -506,37 +517,40 @@ __global__ void __launch_bounds__(64 * NW * KS) ring8_kernel(G8 p) {
       af[s] = cat8(lds128(sub + frag0), lds128(sub + frag1));
       if constexpr (WX128) af[s] = flip80(af[s]);
     }
-    float sa = 0.f, sw[NT][4];
+    float sa[MT], sw[NT][4];
     if constexpr (SCALES) {
       const float* sl = reinterpret_cast<const float*>(st + SC_OFF);
-      sa = sl[r16];
+#pragma unroll
+      for (int t = 0; t < MT; ++t) sa[t] = sl[16 * t + r16];
 #pragma unroll
       for (int s = 0; s < NT; ++s)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          sw[s][i] = KIND == kFp8Block ? sl[16 + wave * NT + s] : sl[16 + 16 * s + 4 * g4 + i];
+          sw[s][i] = KIND == kFp8Block ? sl[SAL + wave * NT + s] : sl[SAL + 16 * s + 4 * g4 + i];
     }
     // The slot consumed last step is free: every wave has passed this step's
     // barrier, so its fragments are in registers.
     const int next = kb + R - 1;
     if (next < nks) issue(next, slot == 0 ? R - 1 : slot - 1);
 #pragma unroll
-    for (int s = 0; s < NT; ++s) {
-      if constexpr (KIND == kFp8Block) {
-        const v4f part = mfma_fp8(af[s], bf, v4f{0.f, 0.f, 0.f, 0.f});
-        const float c = sw[s][0] * sa;
+    for (int s = 0; s < NT; ++s)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[s][i] = fmaf(part[i], c, acc[s][i]);
-      } else if constexpr (KIND == kI8Token) {
-        acci[s] = mfma_i8(lo4(af[s]), lo4(bf), acci[s]);
-        acci[s] = mfma_i8(hi4(af[s]), hi4(bf), acci[s]);
-      } else {
-        v4i part = mfma_i8(lo4(af[s]), lo4(bf), v4i{0, 0, 0, 0});
-        part = mfma_i8(hi4(af[s]), hi4(bf), part);
+      for (int t = 0; t < MT; ++t) {
+        if constexpr (KIND == kFp8Block) {
+          const v4f part = mfma_fp8(af[s], bf[t], v4f{0.f, 0.f, 0.f, 0.f});
+          const float c = sw[s][0] * sa[t];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[s][i] = fmaf((float)part[i], sw[s][i] * sa, acc[s][i]);
+          for (int i = 0; i < 4; ++i) acc[s][t][i] = fmaf(part[i], c, acc[s][t][i]);
+        } else if constexpr (KIND == kI8Token) {
+          acci[s][t] = mfma_i8(lo4(af[s]), lo4(bf[t]), acci[s][t]);
+          acci[s][t] = mfma_i8(hi4(af[s]), hi4(bf[t]), acci[s][t]);
+        } else {
+          v4i part = mfma_i8(lo4(af[s]), lo4(bf[t]), v4i{0, 0, 0, 0});
+          part = mfma_i8(hi4(af[s]), hi4(bf[t]), part);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[s][t][i] = fmaf((float)part[i], sw[s][i] * sa[t], acc[s][t][i]);
+        }
       }
-    }
     slot = slot == R - 1 ? 0 : slot + 1;
   }
 
@@ -547,8 +561,10 @@ __global__ void __launch_bounds__(64 * NW * KS) ring8_kernel(G8 p) {
 #pragma unroll
     for (int s2 = 0; s2 < NT; ++s2)
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        red[(s2 * 4 + i) * 64 + lane] = INT_ACC ? __int_as_float(acci[s2][i]) : acc[s2][i];
+      for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          red[((s2 * MT + t) * 4 + i) * 64 + lane] = INT_ACC ? __int_as_float(acci[s2][t][i]) : acc[s2][t][i];
     __syncthreads();
     if (kw != 0) return;
 #pragma unroll
@@ -557,28 +573,33 @@ __global__ void __launch_bounds__(64 * NW * KS) ring8_kernel(G8 p) {
 #pragma unroll
       for (int s2 = 0; s2 < NT; ++s2)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float v = rw[(s2 * 4 + i) * 64 + lane];
-          if constexpr (INT_ACC) acci[s2][i] += __float_as_int(v);
-          else acc[s2][i] += v;
-        }
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float v = rw[((s2 * MT + t) * 4 + i) * 64 + lane];
+            if constexpr (INT_ACC) acci[s2][t][i] += __float_as_int(v);
+            else acc[s2][t][i] += v;
+          }
     }
   }
 
   if (nout0 >= p.n_out) return;
-  int brow, orow;
-  bool bval;
-  token_row<MOE>(p, m0 + r16, brow, orow, bval);
 #pragma unroll
-  for (int so = 0; so < NTH; ++so) {
-    float g[4], u[4];
+  for (int t = 0; t < MT; ++t) {
+    int brow, orow;
+    bool bval;
+    token_row<MOE>(p, m0 + 16 * t + r16, brow, orow, bval);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      g[i] = INT_ACC ? __int_as_float(acci[so][i]) : acc[so][i];
-      if constexpr (GATED) u[i] = INT_ACC ? __int_as_float(acci[so + NTH][i]) : acc[so + NTH][i];
-      else u[i] = 0.f;
+    for (int so = 0; so < NTH; ++so) {
+      float g[4], u[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        g[i] = INT_ACC ? __int_as_float(acci[so][t][i]) : acc[so][t][i];
+        if constexpr (GATED) u[i] = INT_ACC ? __int_as_float(acci[so + NTH][t][i]) : acc[so + NTH][t][i];
+        else u[i] = 0.f;
+      }
+      finish4<KIND, EPI, ACT, MOE>(p, orow, brow, bval, nout0 + 16 * so + 4 * g4, g, u);
     }
-    finish4<KIND, EPI, ACT, MOE>(p, orow, brow, bval, nout0 + 16 * so + 4 * g4, g, u);
   }
 }
 
@@ -905,35 +926,43 @@ int launch_stream(const G8& p, int grid_y, hipStream_t st, const char* op) {
 // INT8 N=K=5120 at M=1 9.1 -> 7.6 us with the split, FP8 N=17408 K=5120 at
 // M=1 20.2 -> 22.1 us with a two-way split).
 //
-// With one token copy per step (M <= 8) the split is taken while every block
-// stays resident in one round (160 KiB of LDS per CU). With two token copies
-// (M 9..32) it pays only on short K (measured: INT8 N=K=5120 at M=32 10.9 ->
+// With one or four token copies per step (M <= 8, M 17..32) the split is
+// taken while every block stays resident in one round (160 KiB of LDS per
+// CU). With two token copies (M 9..16) it pays only on short K (measured: INT8 N=K=5120 at M=32 10.9 ->
 // 10.1 us with four waves; FP8 N=5120 K=17408 at M=16 28 -> 32-36 us with two
 // or four), so there it needs K <= 8192.
-inline int ring_ksplit(const G8& p, int64_t waves, int64_t blocks, int64_t ring_bytes, bool tq1) {
+inline int ring_ksplit(const G8& p, int64_t waves, int64_t blocks, int64_t ring_bytes, int tq) {
   const int nks = p.K >> 7;
   const int64_t cus = cu_count();
   if (waves >= 4 * cus) return 1;
   const int top = nks >= 16 ? 4 : nks >= 8 ? 2 : 1;
-  if (!tq1) return nks <= 64 ? top : 1;
+  if (tq == 2) return nks <= 64 ? top : 1;
   const int64_t per_cu = (blocks + cus - 1) / cus;
   for (int ks = top; ks > 1; ks /= 2)
     if (per_cu * ks * ring_bytes <= 160 * 1024) return ks;
   return 1;
 }
 
-template <int KIND, int NT, bool MOE, int EPI, int ACT, int R, bool WX128, int NW, bool SPLIT = false>
+// T32: dense blocks of 17..32 token rows take two token subtiles per wave
+// (weights streamed once); otherwise a block covers 16 rows (grid_y given).
+template <int KIND, int NT, bool MOE, int EPI, int ACT, int R, bool WX128, int NW, bool SPLIT = false,
+          bool T32 = false>
 int launch_ring(const G8& p, int grid_y, hipStream_t st, const char* op) {
   constexpr int NTH = (EPI == kEpiGated) ? NT / 2 : NT;
   const int groups = (p.n_out + 16 * NTH - 1) / (16 * NTH);
   const int grid_x = (groups + NW - 1) / NW;
-  const bool tq1 = !MOE && p.M <= 8;
+  // 32-row token subtiles pay when the columns alone give four waves per CU;
+  // below that, two 16-row groups with the K split run faster (measured:
+  // INT8 N=K=5120 at M=32 10.1 vs 11.8 us; FP8 N=17408 K=5120 at M=32 35 vs
+  // 31 us the other way).
+  const bool t32 = T32 && !MOE && NW == 1 && p.M > 16 && (int64_t)grid_x * ((p.M + 31) / 32) >= 4LL * cu_count();
+  const int tq = (!MOE && p.M <= 8) ? 1 : (t32 ? 4 : 2);
+  if (tq == 4) grid_y = (p.M + 31) / 32;
   int ks = 1;
   if constexpr (SPLIT && NW == 1) {
     constexpr bool SCALES = (KIND != kI8Token);
-    const int64_t tq = tq1 ? 1 : 2;
     const int64_t ring_bytes = (int64_t)R * (NT * 2048 + tq * 1024 + (SCALES ? 256 : 0));
-    ks = ring_ksplit(p, (int64_t)grid_x * grid_y, (int64_t)grid_x * grid_y, ring_bytes, tq1);
+    ks = ring_ksplit(p, (int64_t)grid_x * grid_y, (int64_t)grid_x * grid_y, ring_bytes, tq);
   }
   auto go = [&](auto tq_tag, auto ks_tag) {
     constexpr int TQ_ = decltype(tq_tag)::value;
@@ -942,8 +971,13 @@ int launch_ring(const G8& p, int grid_y, hipStream_t st, const char* op) {
                        dim3(64 * NW * KS_), 0, st, p);
   };
   auto with_tq = [&](auto ks_tag) {
-    if (tq1) go(std::integral_constant<int, 1>{}, ks_tag);
-    else go(std::integral_constant<int, 2>{}, ks_tag);
+    if (tq == 1) go(std::integral_constant<int, 1>{}, ks_tag);
+    else if constexpr (T32 && !MOE && NW == 1) {
+      if (tq == 4) go(std::integral_constant<int, 4>{}, ks_tag);
+      else go(std::integral_constant<int, 2>{}, ks_tag);
+    } else {
+      go(std::integral_constant<int, 2>{}, ks_tag);
+    }
   };
   if constexpr (SPLIT && NW == 1) {
     if (ks == 4) with_tq(std::integral_constant<int, 4>{});
@@ -1023,7 +1057,7 @@ int dense_dispatch(const G8& p, hipStream_t st, const char* op, int cfg) {
     else cfg = 6;
   }
   switch (cfg) {
-    case 0: return launch_ring<KIND, 1, false, EPI, kActSilu, 5, WX128, 1, true>(p, (M + 15) / 16, st, op);
+    case 0: return launch_ring<KIND, 1, false, EPI, kActSilu, 5, WX128, 1, true, true>(p, (M + 15) / 16, st, op);
     case 1: return launch_stream<KIND, 1, 2, 4, false, EPI, kActSilu, 4, WX128>(p, (M + 31) / 32, st, op);
     case 2: return launch_stream<KIND, 1, 4, 4, false, EPI, kActSilu, 2, WX128>(p, (M + 63) / 64, st, op);
     case 3: return launch_tiled<KIND, 128, 128, 2, 2, 4, false, EPI, kActSilu, WX128>(p, 0, st, op);
