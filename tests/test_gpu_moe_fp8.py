@@ -139,6 +139,39 @@ def test_expert_gemm(tokens, block_m, gemm, activation, small_experts):
     assert peak_rel_err(c, ref) <= TOL
 
 
+@pytest.mark.parametrize("block_m", [128, 256])
+@pytest.mark.parametrize("gemm", ["w13", "w2"])
+def test_expert_gemm_ragged_columns(block_m, gemm):
+    """Column counts that are not a multiple of the 256-column tile (gated
+    halves of 384, three 128-column halves; a w2 of 384 rows), experts
+    holding more than one block. (Gated FP8-block halves must be whole
+    128-row scale blocks.)"""
+    e, k_top, t, inter, h = 4, 2, 700, 384, 384
+    g = torch.Generator().manual_seed(block_m + len(gemm))
+    ids = torch.stack([torch.randperm(e, generator=g)[:k_top] for _ in range(t)]).to(torch.int32)
+    if gemm == "w13":
+        n, k_in, a_rows, a_topk = 2 * inter, h, t, k_top
+    else:
+        n, k_in, a_rows, a_topk = h, inter, t * k_top, 1
+    w = (torch.randn(e, n, k_in, generator=g) * 0.02)
+    wq, ws = workloads.quantize_fp8_block(w)
+    deq = torch.stack([oracle.fp8_block_dequant(wq[i], ws[i]) for i in range(e)])
+    a = torch.randn(a_rows, k_in, generator=g).to(torch.bfloat16)
+    weights = None if gemm == "w13" else torch.rand(t, k_top, generator=g)
+    qa, sa = oracle.fp8_quant_group128(a)
+    sorted_ids, expert_ids, num_post = torch.ops.strix.moe_align(ids.to(DEV), e, block_m)
+    cols = inter if gemm == "w13" else n
+    c = torch.full((t * k_top, cols), float("nan"), dtype=torch.bfloat16, device=DEV)
+    torch.ops.strix.moe_gemm_fp8_w8a8(c, qa.to(DEV), sa.to(DEV), wq.to(DEV), ws.to(DEV), sorted_ids, expert_ids,
+                                      num_post, None if weights is None else weights.reshape(-1).to(DEV), a_topk,
+                                      block_m, 64, gemm == "w13", "silu")
+    ref = oracle.moe_expert_gemm(qa.float() * sa.repeat_interleave(128, dim=1), deq, ids, a_topk, weights)
+    if gemm == "w13":
+        ref = torch.nn.functional.silu(ref[:, :inter]) * ref[:, inter:]
+    assert not torch.isnan(c).any()
+    assert peak_rel_err(c, ref) <= TOL
+
+
 # ---------------------------------------------------------------- fused, config 3
 @pytest.fixture(scope="module")
 def c3_weights():
