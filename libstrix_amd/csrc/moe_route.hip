@@ -309,7 +309,7 @@ __global__ void __launch_bounds__(1024)
     align_scan_kernel(int32_t* __restrict__ hist, int chunks, int S, int E, int block_m,
                       int32_t* __restrict__ sorted_ids, int64_t sorted_cap, int32_t* __restrict__ expert_ids,
                       int64_t blocks_cap, int32_t* __restrict__ num_post) {
-  extern __shared__ int32_t sm[];  // [parts][E] partial counts, then [E] offsets, [16] wave totals
+  extern __shared__ int32_t sm[];  // [parts][E] partial counts, [E] offsets, [16] wave totals, [E] counts
   const int parts = max(1, 1024 / E);
   const int cpp = (chunks + parts - 1) / parts;
   int32_t* psum = sm;
@@ -323,10 +323,12 @@ __global__ void __launch_bounds__(1024)
   int local = 0;
   {
     int c = c0;
-    for (; c + 4 <= c1; c += 4) {
-      const int a = hist[(int64_t)c * E + e], b = hist[(int64_t)(c + 1) * E + e];
-      const int d = hist[(int64_t)(c + 2) * E + e], f = hist[(int64_t)(c + 3) * E + e];
-      local += a + b + d + f;
+    for (; c + 8 <= c1; c += 8) {
+      int h[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) h[j] = hist[(int64_t)(c + j) * E + e];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) local += h[j];
     }
     for (; c < c1; ++c) local += hist[(int64_t)c * E + e];
   }
@@ -341,10 +343,17 @@ __global__ void __launch_bounds__(1024)
   const int total = wave_tot[15];
   if (tid == 0) num_post[0] = total;
   __syncthreads();
-  // Padding fill: each expert's tail, then everything past the last run
-  // (disjoint from the slots the scatter pass writes).
-  if (tid < E) {
-    for (int i = cnt; i < padded; ++i) sorted_ids[off[tid] + i] = S;
+  // Padding fill: each expert's tail, `parts` threads per expert striding over
+  // it, then everything past the last run (disjoint from the slots the scatter
+  // pass writes). Counts go through LDS, since thread e owns count e.
+  int32_t* cnt_l = wave_tot + 16;
+  if (tid < E) cnt_l[tid] = cnt;
+  __syncthreads();
+  if (tid < parts * E) {
+    const int pe = tid / parts, pq = tid - pe * parts;
+    const int c2 = cnt_l[pe];
+    const int pad2 = (c2 + block_m - 1) / block_m * block_m;
+    for (int i = c2 + pq; i < pad2; i += parts) sorted_ids[off[pe] + i] = S;
   }
   for (int64_t i = total + tid; i < sorted_cap; i += 1024) sorted_ids[i] = S;
   for (int64_t b = tid; b < blocks_cap; b += 1024) {
@@ -362,10 +371,23 @@ __global__ void __launch_bounds__(1024)
     expert_ids[b] = ex;
   }
   // Chunk bases: expert offset + this part's predecessors + running count.
+  // Eight chunks' counts are loaded before any base is written back, so the
+  // walk pays one memory latency per eight chunks.
   if (owner) {
     int run = off[e];
     for (int q = 0; q < part; ++q) run += psum[q * E + e];
-    for (int c = c0; c < c1; ++c) {
+    int c = c0;
+    for (; c + 8 <= c1; c += 8) {
+      int h[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) h[j] = hist[(int64_t)(c + j) * E + e];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        hist[(int64_t)(c + j) * E + e] = run;
+        run += h[j];
+      }
+    }
+    for (; c < c1; ++c) {
       const int64_t i = (int64_t)c * E + e;
       const int n = hist[i];
       hist[i] = run;
@@ -401,18 +423,26 @@ __global__ void __launch_bounds__(256)
   if (t >= T) return;
   const int h = (int)(idx % hv) * 8;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int j = 0; j < k; ++j) {
-    const u32x4 raw = *reinterpret_cast<const u32x4*>(y + (t * k + j) * ldy + h);
-    const float wj = w ? w[t * k + j] : 1.0f;
+  // Four rows' loads in flight before any is used; the sum stays in row order.
+  for (int j0 = 0; j0 < k; j0 += 4) {
+    u32x4 raw[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float lo = act_to_f32<F16>(raw[i] & 0xffffu), hi = act_to_f32<F16>(raw[i] >> 16);
-      if (w) {
-        acc[2 * i] = fmaf(wj, lo, acc[2 * i]);
-        acc[2 * i + 1] = fmaf(wj, hi, acc[2 * i + 1]);
-      } else {
-        acc[2 * i] += lo;
-        acc[2 * i + 1] += hi;
+    for (int q = 0; q < 4; ++q)
+      if (j0 + q < k) raw[q] = *reinterpret_cast<const u32x4*>(y + (t * k + j0 + q) * ldy + h);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (j0 + q >= k) break;
+      const float wj = w ? w[t * k + j0 + q] : 1.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float lo = act_to_f32<F16>(raw[q][i] & 0xffffu), hi = act_to_f32<F16>(raw[q][i] >> 16);
+        if (w) {
+          acc[2 * i] = fmaf(wj, lo, acc[2 * i]);
+          acc[2 * i + 1] = fmaf(wj, hi, acc[2 * i + 1]);
+        } else {
+          acc[2 * i] += lo;
+          acc[2 * i + 1] += hi;
+        }
       }
     }
   }
@@ -502,7 +532,7 @@ int strix_moe_align(const int32_t* topk_ids, int64_t num_slots, int64_t E, int64
   int rc = check_launch(op);
   if (rc) return rc;
   const int parts = (int)std::max<int64_t>(1, 1024 / E);
-  const size_t scan_lds = ((size_t)parts * E + E + 16) * 4;
+  const size_t scan_lds = ((size_t)parts * E + 2 * E + 16) * 4;
   hipLaunchKernelGGL(align_scan_kernel, dim3(1), dim3(1024), scan_lds, st, hist, chunks, S, (int)E,
                      (int)block_m, sorted_ids, sorted_cap, expert_ids, blocks_cap, num_post);
   rc = check_launch(op);

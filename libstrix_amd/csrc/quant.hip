@@ -10,8 +10,10 @@
 //                       q[m,k]  = e4m3_rne(x[m,k] / s[m,g])
 //
 // The division is IEEE (correctly rounded), so the CPU oracle reproduces q
-// bit for bit. Each lane owns 8 consecutive elements (one 16-byte load); a
-// 128-group is 16 lanes, so the group max is a 16-lane butterfly.
+// bit for bit; the e4m3 quantizer gets the same bytes from a reciprocal
+// product, with the division kept where the product could round differently. In the 128-group quantizers each lane owns 16 consecutive
+// elements (two 16-byte loads); a group is 8 lanes, so the group max is an
+// 8-lane butterfly.
 #include "capi_internal.h"
 #include "strix_common.h"
 
@@ -26,6 +28,21 @@ __device__ __forceinline__ void load8(const uint16_t* p, float v[8]) {
     v[2 * i] = act_to_f32<F16>(raw[i] & 0xffffu);
     v[2 * i + 1] = act_to_f32<F16>(raw[i] >> 16);
   }
+}
+
+// x / sc correctly rounded, as far as the e4m3 rounding that follows can
+// tell. x * RN(1/sc) is within 1.5 ulp of x / sc, so both round to the same
+// e4m3 value unless the product lies in e4m3's subnormal range or within 4
+// ulp of an e4m3 rounding midpoint (low 20 mantissa bits near 0x80000); those
+// elements, and groups whose scale is subnormal (1/sc would overflow), take
+// the IEEE division. tests/test_e4m3_quotient.py checks the argument on the
+// CPU for every 16-bit x against sampled group maxima.
+__device__ __forceinline__ float div_for_e4m3(float x, float sc, float r, bool fast) {
+  float q = x * r;
+  const uint32_t b = __float_as_uint(q) & 0x7fffffffu;
+  const int d = (int)(b & 0xfffffu) - 0x80000;
+  if (!fast || b - 1u < (121u << 23) - 1u || (unsigned)(d + 4) <= 8u) q = __fdiv_rn(x, sc);
+  return q;
 }
 
 __device__ __forceinline__ int q_i8(float x, float s) {
@@ -68,57 +85,62 @@ __global__ void __launch_bounds__(256)
   }
 }
 
-// 128-element groups. Thread t of the grid handles elements [8t, 8t+8) of
-// the flattened [M, K] view (row-major by groups), 16 lanes per group.
+// 128-element groups. Thread t of the grid handles elements [16t, 16t+16) of
+// the flattened [M, K] view (row-major by groups), 8 lanes per group: two
+// 16-byte loads in flight per lane, and the group's (row, column) from one
+// 32-bit division (the host bounds the group count below 2^28).
 // FP8 selects the e4m3 quantizer, otherwise int8.
 template <bool F16, bool FP8>
 __global__ void __launch_bounds__(256)
     quant_group128_kernel(const uint16_t* __restrict__ x, int64_t ldx, uint8_t* __restrict__ q,
-                          int64_t ldq, float* __restrict__ s, int64_t lds, int groups_per_row,
-                          int64_t total_groups) {
-  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t grp = t >> 4;
-  const int sub = t & 15;
+                          int64_t ldq, float* __restrict__ s, int64_t lds, uint32_t groups_per_row,
+                          uint32_t total_groups) {
+  const uint32_t t = blockIdx.x * 256u + threadIdx.x;
+  const uint32_t grp = t >> 3;
+  const int sub = (int)(t & 7u);
   const bool live = grp < total_groups;
-  const int64_t m = live ? grp / groups_per_row : 0;
-  const int g = live ? (int)(grp % groups_per_row) : 0;
-  const int64_t k = (int64_t)g * 128 + sub * 8;
-  float v[8];
+  const uint32_t m = live ? grp / groups_per_row : 0u;
+  const uint32_t g = live ? grp - m * groups_per_row : 0u;
+  const int64_t k = (int64_t)g * 128 + sub * 16;
+  float v[16];
   if (live) {
-    load8<F16>(x + m * ldx + k, v);
+    const uint16_t* p = x + (int64_t)m * ldx + k;
+    load8<F16>(p, v);
+    load8<F16>(p + 8, v + 8);
   } else {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+    for (int i = 0; i < 16; ++i) v[i] = 0.0f;
   }
   float mx = 0.0f;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(v[i]));
+  for (int i = 0; i < 16; ++i) mx = fmaxf(mx, fabsf(v[i]));
 #pragma unroll
-  for (int o = 8; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
+  for (int o = 4; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
   const float qmax = FP8 ? 448.0f : 127.0f;
   const float sc = mx > 0.0f ? __fdiv_rn(mx, qmax) : 1.0f;
   if (!live) return;
-  if (sub == 0) s[m * lds + g] = sc;
-  uint32_t lo = 0, hi = 0;
-  if constexpr (FP8) {
-    int w0 = 0, w1 = 0;
-    w0 = cvt_pk_e4m3<false>(__fdiv_rn(v[0], sc), __fdiv_rn(v[1], sc), w0);
-    w0 = cvt_pk_e4m3<true>(__fdiv_rn(v[2], sc), __fdiv_rn(v[3], sc), w0);
-    w1 = cvt_pk_e4m3<false>(__fdiv_rn(v[4], sc), __fdiv_rn(v[5], sc), w1);
-    w1 = cvt_pk_e4m3<true>(__fdiv_rn(v[6], sc), __fdiv_rn(v[7], sc), w1);
-    lo = (uint32_t)w0;
-    hi = (uint32_t)w1;
-  } else {
+  if (sub == 0) s[(int64_t)m * lds + g] = sc;
+  const bool fast = sc >= 0x1p-126f;
+  const float rs = FP8 ? __fdiv_rn(1.0f, sc) : 0.0f;
+  uint32_t w[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) lo |= (uint32_t)(q_i8(v[i], sc) & 0xff) << (8 * i);
+  for (int j = 0; j < 4; ++j) {
+    const float* u = v + 4 * j;
+    if constexpr (FP8) {
+      int r = 0;
+      r = cvt_pk_e4m3<false>(div_for_e4m3(u[0], sc, rs, fast), div_for_e4m3(u[1], sc, rs, fast), r);
+      r = cvt_pk_e4m3<true>(div_for_e4m3(u[2], sc, rs, fast), div_for_e4m3(u[3], sc, rs, fast), r);
+      w[j] = (uint32_t)r;
+    } else {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) hi |= (uint32_t)(q_i8(v[4 + i], sc) & 0xff) << (8 * i);
+      for (int i = 0; i < 4; ++i) w[j] |= (uint32_t)(q_i8(u[i], sc) & 0xff) << (8 * i);
+    }
   }
-  *reinterpret_cast<uint2*>(q + m * ldq + k) = make_uint2(lo, hi);
+  uint2* out = reinterpret_cast<uint2*>(q + (int64_t)m * ldq + k);  // output rows are 8-byte aligned
+  out[0] = make_uint2(w[0], w[1]);
+  out[1] = make_uint2(w[2], w[3]);
 }
 
-// out[m, k] = q[m, k] * s[m, k / 128] rounded to the 16-bit output type: the
-// activations an int8 x int4 GEMM multiplies, handed to a 16-bit MFMA GEMM.
 template <bool F16>
 __global__ void __launch_bounds__(256)
     int8_dequant_group128_kernel(const int8_t* __restrict__ q, int64_t ldq, const float* __restrict__ s,
@@ -190,26 +212,29 @@ static int quant_group128(const char* op, bool fp8, const void* x, int x_dtype, 
   if (M == 0 || K == 0) return STRIX_OK;
   STRIX_ARCH_GATE();
   const int64_t groups = M * (K / 128);
-  const int64_t threads = groups * 16;
+  STRIX_REQUIRE(groups < (int64_t(1) << 28), "%s: %lld groups of 128 exceed the 2^28 limit", op,
+                (long long)groups);
+  const int64_t threads = groups * 8;
   const unsigned blocks = (unsigned)((threads + 255) / 256);
   const uint16_t* xp = static_cast<const uint16_t*>(x);
   uint8_t* qp = static_cast<uint8_t*>(q);
-  const int gpr = (int)(K / 128);
+  const uint32_t gpr = (uint32_t)(K / 128);
+  const uint32_t ngroups = (uint32_t)groups;
   hipStream_t st = as_stream(stream);
   if (fp8) {
     if (x_dtype == STRIX_F16)
       hipLaunchKernelGGL((quant_group128_kernel<true, true>), dim3(blocks), dim3(256), 0, st, xp,
-                         ldx, qp, ldq, s, lds, gpr, groups);
+                         ldx, qp, ldq, s, lds, gpr, ngroups);
     else
       hipLaunchKernelGGL((quant_group128_kernel<false, true>), dim3(blocks), dim3(256), 0, st, xp,
-                         ldx, qp, ldq, s, lds, gpr, groups);
+                         ldx, qp, ldq, s, lds, gpr, ngroups);
   } else {
     if (x_dtype == STRIX_F16)
       hipLaunchKernelGGL((quant_group128_kernel<true, false>), dim3(blocks), dim3(256), 0, st, xp,
-                         ldx, qp, ldq, s, lds, gpr, groups);
+                         ldx, qp, ldq, s, lds, gpr, ngroups);
     else
       hipLaunchKernelGGL((quant_group128_kernel<false, false>), dim3(blocks), dim3(256), 0, st, xp,
-                         ldx, qp, ldq, s, lds, gpr, groups);
+                         ldx, qp, ldq, s, lds, gpr, ngroups);
   }
   return check_launch(op);
 }
