@@ -170,10 +170,17 @@ def point_c2(torch, S, timer, m, weights):
            "tflops": round(flops / us_k / 1e6, 1), "gbs": round(by / us_k / 1e3, 1),
            "frac_fp8_mfma": round(flops / us_k / 1e6 / PEAK_FP8_TFLOPS, 4),
            "frac_hbm": round(by / us_k / 1e3 / PEAK_HBM_GBS, 4), "cold_weight_sets": len(sets)}
+    # The plugin's layout: the same weights K-block-major (weight8_kmajor), same bits.
+    ksets = [(S.weight8_kmajor(w), sw) for (w, sw) in sets]
+    us_kk = timer(lambda i: S.fp8_w8a8_block_gemm_kmajor(q, s, *ksets[i % len(ksets)]), iters=max(20, 3 * len(sets)))
+    res.update({"kmajor_gemm_us": round(us_kk, 2), "kmajor_tflops": round(flops / us_kk / 1e6, 1),
+                "kmajor_frac_hbm": round(by / us_kk / 1e3 / PEAK_HBM_GBS, 4)})
     if m <= 16:
         fns = [lambda w=w, sw=sw: S.fp8_w8a8_block_gemm(*S.fp8_quant_group128(x), w, sw) for (w, sw) in sets]
         res["op_graph_us"] = round(graph_us(torch, fns), 2)
-    del sets
+        fns = [lambda w=w, sw=sw: S.fp8_w8a8_block_gemm_kmajor(*S.fp8_quant_group128(x), w, sw) for (w, sw) in ksets]
+        res["kmajor_op_graph_us"] = round(graph_us(torch, fns), 2)
+    del sets, ksets
     return res
 
 

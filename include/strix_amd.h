@@ -80,6 +80,21 @@ int strix_fp8_w8a8_block_gemm(const uint8_t* qa, int64_t lda, const float* sa, i
                               const uint8_t* w, int64_t ldw, const float* sw, int64_t sw_ld,
                               void* out, int64_t ldo, int out_dtype, int64_t M, int64_t N,
                               int64_t K, int cfg, void* stream);
+/* 8-bit weights [E][N][ldw] -> K-block-major [E][K/128][N][128] (one
+ * contiguous run per 128-K block of all rows). No counterpart in the
+ * reference, whose kernels read row-major weights: a one-time weight
+ * preparation in the place of the plugin's weight processing, which
+ * re-strides FP8 weights for the memory system's sake
+ * (python/strix_vllm/fp8.py:147-160), for the *_kmajor GEMM below. */
+int strix_weight8_kmajor(const uint8_t* w, int64_t ldw, int64_t E, int64_t N, int64_t K, uint8_t* out,
+                         void* stream);
+/* strix_fp8_w8a8_block_gemm on K-block-major weights (w_kmajor[kb][n][128]),
+ * bit-identical output. The concurrently streamed weight blocks sit together
+ * in memory, which DRAM serves faster at decode. */
+int strix_fp8_w8a8_block_gemm_kmajor(const uint8_t* qa, int64_t lda, const float* sa, int64_t sa_ld,
+                                     const uint8_t* w_kmajor, const float* sw, int64_t sw_ld, void* out,
+                                     int64_t ldo, int out_dtype, int64_t M, int64_t N, int64_t K, int cfg,
+                                     void* stream);
 /* INT8 per-token W8A8: out = bf16((float(qa.qw) * sa[m]) * sw[n]); out_dtype
  * STRIX_I32 writes the raw int32 accumulator (the bit-exactness probe). The
  * per-token sibling of w8a8_wmma_gemm (csrc/gemm/w8a8_wmma_gemm.hip:799-918). */
@@ -105,6 +120,15 @@ int strix_moe_gemm_fp8_w8a8(void* c, int64_t ldc, int c_dtype, const uint8_t* qa
                             const int32_t* num_post, const float* topk_weights, int64_t num_slots,
                             int64_t top_k, int64_t block_m, int silu_mul, int activation, int64_t N,
                             int64_t K, void* stream);
+/* strix_moe_gemm_fp8_w8a8 on K-block-major expert weights
+ * w_kmajor[E][K/128][N][128] (strix_weight8_kmajor with E experts),
+ * bit-identical output. */
+int strix_moe_gemm_fp8_w8a8_kmajor(void* c, int64_t ldc, int c_dtype, const uint8_t* qa, int64_t lda,
+                                   const float* sa, int64_t sa_ld, const uint8_t* w_kmajor, const float* sw,
+                                   int64_t sw_es, int64_t sw_ns, const int32_t* sorted_ids, int64_t sorted_len,
+                                   const int32_t* expert_ids, int64_t num_blocks, const int32_t* num_post,
+                                   const float* topk_weights, int64_t num_slots, int64_t top_k, int64_t block_m,
+                                   int silu_mul, int activation, int64_t N, int64_t K, void* stream);
 
 /* ------------------------------------------------------------------ 16-bit MFMA GEMMs over dequantized weights
  * Common MoE arguments (STRIX_MOE16_ARGS in gemm16.hip): c [num_slots, ldc]

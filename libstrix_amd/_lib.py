@@ -41,9 +41,12 @@ SIGNATURES: dict[str, list] = {
     "strix_int8_dequant_group128": [P, L, P, L, P, I, L, L, L, P],
     "strix_w16_gemm": [I, P, L, P, I, L, L, L, L, P, I, L, P, L, P, L, I, L, L, L, I, P],
     "strix_fp8_w8a8_block_gemm": [P, L, P, L, P, L, P, L, P, L, I, L, L, L, I, P],
+    "strix_weight8_kmajor": [P, L, L, L, L, P, P],
+    "strix_fp8_w8a8_block_gemm_kmajor": [P, L, P, L, P, P, L, P, L, I, L, L, L, I, P],
     "strix_w8a8_int8_gemm": [P, L, P, P, L, P, P, L, I, L, L, L, I, P],
     "strix_w8a8_int8_group_gemm": [P, L, P, L, P, L, I, P, L, L, P, L, I, L, L, L, I, P],
     "strix_moe_gemm_fp8_w8a8": [P, L, I, P, L, P, L, P, L, L, P, L, L, P, L, P, L, P, P, L, L, L, I, I, L, L, P],
+    "strix_moe_gemm_fp8_w8a8_kmajor": [P, L, I, P, L, P, L, P, P, L, L, P, L, P, L, P, P, L, L, L, I, I, L, L, P],
     "strix_moe_gemm_mxfp4": [P, L, L, P, L, L] + MOE16,
     "strix_moe_gemm_w4a16_zp": [P, L, L, P, I, L, L, P, L, L, L] + MOE16,
     "strix_moe_gemm_w4a16": [P, L, L, P, I, L, L, L] + MOE16,

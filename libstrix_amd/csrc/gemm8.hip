@@ -29,8 +29,9 @@ namespace {
 enum Kind8 : int { kFp8Block = 0, kI8Token = 1, kI8Group = 2 };
 
 struct G8 {
-  const uint8_t* w;  // weight bytes [E][N][ldw]
+  const uint8_t* w;  // weight bytes: row n, K block kb at n * ldw + kb * w_kbs
   int64_t ldw, w_es;
+  int64_t w_kbs = 128;  // row-major [E][N][ldw]: 128; K-block-major [E][K/128][N][128]: 128 * N
   const float* sw;   // fp8: [E][ceil(N/128)][K/128]; i8: [E][N][G] (G may be 1)
   int64_t sw_es, sw_ns, sw_ks;
   const uint8_t* a;  // activation bytes [rows][lda]
@@ -189,9 +190,9 @@ __global__ void __launch_bounds__(256) stream8_kernel(G8 p) {
 
   using F = Frag8<NT, MT>;
   auto load = [&](int kb, F& f) {
-    const int64_t ko = (int64_t)kb * 128;
+    const int64_t ko = (int64_t)kb * 128, kw = (int64_t)kb * p.w_kbs;
 #pragma unroll
-    for (int s = 0; s < NT; ++s) f.af[s] = cat8(ldg128(wp[s] + ko), ldg128(wp[s] + ko + 64));
+    for (int s = 0; s < NT; ++s) f.af[s] = cat8(ldg128(wp[s] + kw), ldg128(wp[s] + kw + 64));
     if constexpr (!TOKL) {
 #pragma unroll
       for (int t = 0; t < MT; ++t) f.bf[t] = cat8(ldg128(ap[t] + ko), ldg128(ap[t] + ko + 64));
@@ -466,9 +467,9 @@ __global__ void __launch_bounds__(64 * NW * KS) ring8_kernel(G8 p) {
   }
   auto issue = [&](int kb, int slot) {
     uint8_t* st = ring + slot * SLOT;
-    const int64_t ko = (int64_t)kb * 128;
+    const int64_t ko = (int64_t)kb * 128, kw = (int64_t)kb * p.w_kbs;
 #pragma unroll
-    for (int q = 0; q < WQ; ++q) g2l_b128(wsrc[q] + ko, st + wave * NT * 2048 + q * 1024);
+    for (int q = 0; q < WQ; ++q) g2l_b128(wsrc[q] + kw, st + wave * NT * 2048 + q * 1024);
     for (int e = e0; e < e0 + ne; ++e) {
       if (e < TQ) g2l_b128(tsrc[e] + ko, st + TOK_OFF + e * 1024);
       else if constexpr (SCALES) g2l_b32(ssrc + (int64_t)kb * sstride, st + SC_OFF);
@@ -719,12 +720,10 @@ __global__ void __launch_bounds__(WM * WN * 64) tiled8_kernel(G8 p, int tiles_m,
 
   auto issue = [&](int kb, int buf) {
     uint8_t* st = smem + buf * STAGE;
-    const int64_t ko = (int64_t)kb * 128;
+    const uint8_t* wb = wbase + (int64_t)kb * p.w_kbs;
+    const uint8_t* ab = p.a + (int64_t)kb * 128;
 #pragma unroll
-    for (int j = 0; j < QPW; ++j) {
-      const uint8_t* base = qis_w[j] ? wbase : p.a;
-      g2l_b128(base + ko + qoff[j], st + (wave + W * j) * 1024);
-    }
+    for (int j = 0; j < QPW; ++j) g2l_b128((qis_w[j] ? wb : ab) + qoff[j], st + (wave + W * j) * 1024);
     if (has_extra) {
       uint8_t* dst = wave < SA_COPIES ? st + SA_OFF + wave * 256 : st + SW_OFF + (wave - SA_COPIES) * 256;
       g2l_b32(xptr + (int64_t)kb * xstride, dst);
@@ -1093,6 +1092,24 @@ int moe_dispatch(const G8& p, int block_m, int num_blocks, hipStream_t st, const
   }
 }
 
+// Row-major 8-bit weights [E][N][ldw] -> K-block-major [E][K/128][N][128]:
+// every 128-K block of all N rows is one contiguous run. The decode and
+// prefill kernels read weights 128 K at a time, and in this order the blocks
+// all waves read at one moment lie close together in memory instead of one
+// per row group across the whole matrix, which DRAM serves faster. One
+// thread per 16-byte chunk, in output order.
+__global__ void __launch_bounds__(256)
+    weight_kmajor_kernel(const uint8_t* __restrict__ w, int64_t ldw, int64_t N, int64_t kbs,
+                         int64_t chunks, uint8_t* __restrict__ out) {
+  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (c >= chunks) return;
+  const int64_t j = c & 7, row = c >> 3;   // 16-byte chunk within the 128-byte block, global block row
+  const int64_t n = row % N, ekb = row / N;
+  const int64_t e = ekb / kbs, kb = ekb % kbs;
+  const u32x4 v = *reinterpret_cast<const u32x4*>(w + (e * N + n) * ldw + kb * 128 + j * 16);
+  *reinterpret_cast<u32x4*>(out + c * 16) = v;
+}
+
 int check_common(const char* op, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw,
                  const void* a, const void* w) {
   STRIX_REQUIRE(M >= 0 && N >= 0 && K >= 0, "%s: negative size", op);
@@ -1126,6 +1143,42 @@ int strix_fp8_w8a8_block_gemm(const uint8_t* qa, int64_t lda, const float* sa, i
   STRIX_ARCH_GATE();
   G8 p = {};
   p.w = w; p.ldw = ldw; p.w_es = 0;
+  p.sw = sw; p.sw_es = 0; p.sw_ns = sw_ld; p.sw_ks = 1;
+  p.a = qa; p.lda = lda; p.sa = sa; p.sa_rs = sa_ld; p.sa_ks = 1;
+  p.out = out; p.ldo = ldo; p.out_f16 = out_dtype == STRIX_F16;
+  p.M = (int)M; p.N = (int)N; p.K = (int)K; p.n_out = (int)N;
+  return dense_dispatch<kFp8Block, kEpiStore, false>(p, as_stream(stream), op, cfg);
+}
+
+int strix_weight8_kmajor(const uint8_t* w, int64_t ldw, int64_t E, int64_t N, int64_t K, uint8_t* out,
+                         void* stream) {
+  const char* op = "weight8_kmajor";
+  STRIX_REQUIRE(E >= 1 && N >= 0 && K >= 0, "%s: bad sizes", op);
+  STRIX_REQUIRE(K % 128 == 0, "%s: K must be a multiple of 128, got K=%lld", op, (long long)K);
+  STRIX_REQUIRE(ldw >= K && ldw % 16 == 0, "%s: weight row stride must be >= K and a multiple of 16", op);
+  STRIX_REQUIRE(aligned(w, 16) && aligned(out, 16), "%s: weights must be 16-byte aligned", op);
+  if (N == 0 || K == 0) return STRIX_OK;
+  STRIX_ARCH_GATE();
+  const int64_t chunks = E * N * (K / 16);
+  hipLaunchKernelGGL(weight_kmajor_kernel, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, as_stream(stream),
+                     w, ldw, N, K / 128, chunks, out);
+  return check_launch(op);
+}
+
+int strix_fp8_w8a8_block_gemm_kmajor(const uint8_t* qa, int64_t lda, const float* sa, int64_t sa_ld,
+                                     const uint8_t* w_kmajor, const float* sw, int64_t sw_ld, void* out,
+                                     int64_t ldo, int out_dtype, int64_t M, int64_t N, int64_t K, int cfg,
+                                     void* stream) {
+  const char* op = "fp8_w8a8_block_gemm_kmajor";
+  int rc = check_common(op, M, N, K, lda, K, qa, w_kmajor);
+  if (rc) return rc;
+  STRIX_REQUIRE(out_dtype == STRIX_BF16 || out_dtype == STRIX_F16, "%s: output must be bfloat16 or float16", op);
+  STRIX_REQUIRE(sa_ld >= K / 128 && sw_ld >= K / 128, "%s: scale row strides must be >= K/128", op);
+  STRIX_REQUIRE(ldo >= N && ldo % 4 == 0 && aligned(out, 8), "%s: output rows must be >= N, 8-byte aligned", op);
+  if (M == 0 || N == 0) return STRIX_OK;
+  STRIX_ARCH_GATE();
+  G8 p = {};
+  p.w = w_kmajor; p.ldw = 128; p.w_kbs = 128 * N; p.w_es = 0;
   p.sw = sw; p.sw_es = 0; p.sw_ns = sw_ld; p.sw_ks = 1;
   p.a = qa; p.lda = lda; p.sa = sa; p.sa_rs = sa_ld; p.sa_ks = 1;
   p.out = out; p.ldo = ldo; p.out_f16 = out_dtype == STRIX_F16;
@@ -1176,15 +1229,20 @@ int strix_w8a8_int8_group_gemm(const int8_t* qa, int64_t lda, const float* sa, i
   return dense_dispatch<kI8Group, kEpiStore, false>(p, as_stream(stream), op, cfg);
 }
 
-int strix_moe_gemm_fp8_w8a8(void* c, int64_t ldc, int c_dtype, const uint8_t* qa, int64_t lda,
-                            const float* sa, int64_t sa_ld, const uint8_t* w, int64_t w_es, int64_t ldw,
-                            const float* sw, int64_t sw_es, int64_t sw_ns, const int32_t* sorted_ids,
-                            int64_t sorted_len, const int32_t* expert_ids, int64_t num_blocks,
-                            const int32_t* num_post, const float* topk_weights, int64_t num_slots,
-                            int64_t top_k, int64_t block_m, int silu_mul, int activation, int64_t N,
-                            int64_t K, void* stream) {
-  const char* op = "moe_gemm_fp8_w8a8";
-  int rc = check_common(op, num_slots, N, K, lda, ldw, qa, w);
+}  // extern "C"
+
+namespace strix {
+namespace {
+
+// The FP8-block expert GEMM over row-major weights [E][N][ldw] (w_es bytes
+// per expert) or, with kmajor, K-block-major ones [E][K/128][N][128].
+int moe_gemm_fp8(const char* op, void* c, int64_t ldc, int c_dtype, const uint8_t* qa, int64_t lda,
+                 const float* sa, int64_t sa_ld, const uint8_t* w, int64_t w_es, int64_t ldw, bool kmajor,
+                 const float* sw, int64_t sw_es, int64_t sw_ns, const int32_t* sorted_ids, int64_t sorted_len,
+                 const int32_t* expert_ids, int64_t num_blocks, const int32_t* num_post,
+                 const float* topk_weights, int64_t num_slots, int64_t top_k, int64_t block_m, int silu_mul,
+                 int activation, int64_t N, int64_t K, void* stream) {
+  int rc = check_common(op, num_slots, N, K, lda, kmajor ? K : ldw, qa, w);
   if (rc) return rc;
   STRIX_REQUIRE(c_dtype == STRIX_BF16 || c_dtype == STRIX_F16, "%s: output must be bfloat16 or float16", op);
   STRIX_REQUIRE(top_k >= 1, "%s: top_k must be >= 1", op);
@@ -1199,7 +1257,12 @@ int strix_moe_gemm_fp8_w8a8(void* c, int64_t ldc, int c_dtype, const uint8_t* qa
   if (num_blocks == 0 || num_slots == 0 || N == 0) return STRIX_OK;
   STRIX_ARCH_GATE();
   G8 p = {};
-  p.w = w; p.ldw = ldw; p.w_es = w_es;
+  p.w = w;
+  if (kmajor) {
+    p.ldw = 128; p.w_es = N * K; p.w_kbs = 128 * N;
+  } else {
+    p.ldw = ldw; p.w_es = w_es;
+  }
   p.sw = sw; p.sw_es = sw_es; p.sw_ns = sw_ns; p.sw_ks = 1;
   p.a = qa; p.lda = lda; p.sa = sa; p.sa_rs = sa_ld; p.sa_ks = 1;
   p.out = c; p.ldo = ldc; p.out_f16 = c_dtype == STRIX_F16;
@@ -1213,6 +1276,34 @@ int strix_moe_gemm_fp8_w8a8(void* c, int64_t ldc, int c_dtype, const uint8_t* qa
     return moe_dispatch<kFp8Block, kEpiGated, kActSilu>(p, bm, nb, st, op);
   }
   return moe_dispatch<kFp8Block, kEpiStore, kActSilu>(p, bm, nb, st, op);
+}
+
+}  // namespace
+}  // namespace strix
+
+extern "C" {
+
+int strix_moe_gemm_fp8_w8a8(void* c, int64_t ldc, int c_dtype, const uint8_t* qa, int64_t lda,
+                            const float* sa, int64_t sa_ld, const uint8_t* w, int64_t w_es, int64_t ldw,
+                            const float* sw, int64_t sw_es, int64_t sw_ns, const int32_t* sorted_ids,
+                            int64_t sorted_len, const int32_t* expert_ids, int64_t num_blocks,
+                            const int32_t* num_post, const float* topk_weights, int64_t num_slots,
+                            int64_t top_k, int64_t block_m, int silu_mul, int activation, int64_t N,
+                            int64_t K, void* stream) {
+  return moe_gemm_fp8("moe_gemm_fp8_w8a8", c, ldc, c_dtype, qa, lda, sa, sa_ld, w, w_es, ldw, false, sw, sw_es,
+                      sw_ns, sorted_ids, sorted_len, expert_ids, num_blocks, num_post, topk_weights, num_slots,
+                      top_k, block_m, silu_mul, activation, N, K, stream);
+}
+
+int strix_moe_gemm_fp8_w8a8_kmajor(void* c, int64_t ldc, int c_dtype, const uint8_t* qa, int64_t lda,
+                                   const float* sa, int64_t sa_ld, const uint8_t* w_kmajor, const float* sw,
+                                   int64_t sw_es, int64_t sw_ns, const int32_t* sorted_ids, int64_t sorted_len,
+                                   const int32_t* expert_ids, int64_t num_blocks, const int32_t* num_post,
+                                   const float* topk_weights, int64_t num_slots, int64_t top_k, int64_t block_m,
+                                   int silu_mul, int activation, int64_t N, int64_t K, void* stream) {
+  return moe_gemm_fp8("moe_gemm_fp8_w8a8_kmajor", c, ldc, c_dtype, qa, lda, sa, sa_ld, w_kmajor, 0, 0, true,
+                      sw, sw_es, sw_ns, sorted_ids, sorted_len, expert_ids, num_blocks, num_post,
+                      topk_weights, num_slots, top_k, block_m, silu_mul, activation, N, K, stream);
 }
 
 }  // extern "C"

@@ -55,9 +55,11 @@ def route_and_align(logits: torch.Tensor, top_k: int, num_experts: int, block_m:
 def fused_moe_fp8_w8a8(x, logits, w13, w13_s, w2, w2_s, top_k: int, renormalize: bool = True,
                        activation: str = "silu", block_m: int | None = None):
     """FP8-block W8A8 fused MoE (config 3): route -> align -> e4m3 1x128 quant
-    -> w13 (fused act*mul) -> e4m3 quant -> w2 (x top-k weight) -> sum."""
+    -> w13 (fused act*mul) -> e4m3 quant -> w2 (x top-k weight) -> sum.
+    Expert weights are row-major [E, N, K] or K-block-major [E, K/128, N, 128]
+    (weight8_kmajor), with the same result."""
     t, h = x.shape
-    e, n13, _ = w13.shape
+    e, n13 = w13.size(0), (w13.size(2) if w13.dim() == 4 else w13.size(1))
     inter = n13 // 2
     bm = block_m or moe_block_m(t, top_k, e)
     ids, w, sorted_ids, expert_ids, num_post = route_and_align(logits, top_k, e, bm, renormalize)

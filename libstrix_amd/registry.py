@@ -121,7 +121,7 @@ KERNELS: list[Kernel] = [
         "fp8_quant",
         "per (row, 128-element group) e4m3fn: s = max|x|/448 (1 for an all-zero group), q = e4m3_rne(x / s)",
         {"dtype": ("bf16", "fp16"), "group_size": 128},
-        {"lanes_per_group": 16},
+        {"lanes_per_group": 8},
     ),
     # ------------------------------------------------------------ int8 dense
     Kernel(
@@ -170,6 +170,19 @@ KERNELS: list[Kernel] = [
         "fp8_w8a8_block_gemm_cfg",
         "fp8_w8a8_tile_sweep",
         "fp8_w8a8_block_gemm pinned to one tile config (0..11)",
+        {"weight_dtype": "fp8_e4m3", "activation_dtype": "fp8_e4m3", "group_size": 128},
+    ),
+    Kernel(
+        "weight8_kmajor",
+        "weight8_kmajor",
+        "8-bit weights [E, N, K] -> K-block-major [E, K/128, N, 128]: one contiguous run per 128-K block, "
+        "so the blocks the GEMM streams at one moment lie together in memory. K % 128 == 0",
+        {"weight_dtype": ("fp8_e4m3", "int8", "uint8"), "group_size": 128},
+    ),
+    Kernel(
+        "fp8_w8a8_block_gemm_kmajor",
+        "fp8_w8a8_kmajor",
+        "fp8_w8a8_block_gemm on K-block-major weights: the same kernels and tiles, bit-identical output",
         {"weight_dtype": "fp8_e4m3", "activation_dtype": "fp8_e4m3", "group_size": 128},
     ),
     # ------------------------------------------------------------ moe

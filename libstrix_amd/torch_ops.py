@@ -270,6 +270,57 @@ def _(qa, sa, w, sw, cfg):
     return qa.new_empty((qa.size(0), w.size(0)), dtype=torch.bfloat16)
 
 
+_W8_DTYPES = (torch.float8_e4m3fn, torch.int8, torch.uint8)
+
+
+@_define("weight8_kmajor(Tensor w) -> Tensor")
+def weight8_kmajor(w):
+    """8-bit weights [N, K] or [E, N, K] (rows contiguous) -> K-block-major
+    [K/128, N, 128] or [E, K/128, N, 128], the layout the *_kmajor GEMMs read."""
+    _check(w.dtype in _W8_DTYPES and w.dim() in (2, 3) and w.stride(-1) == 1, "w must be 8-bit [N, K] or [E, N, K]")
+    k = w.size(-1)
+    _check(k % 128 == 0, f"K must be a multiple of 128, got K={k}")
+    e, n = (1, w.size(0)) if w.dim() == 2 else (w.size(0), w.size(1))
+    _check(w.dim() == 2 or w.stride(0) == n * w.stride(1), "expert slices must follow each other")
+    shape = (k // 128, n, 128) if w.dim() == 2 else (e, k // 128, n, 128)
+    out = torch.empty(shape, dtype=w.dtype, device=w.device)
+    _lib.call("strix_weight8_kmajor", _ptr(w), w.stride(-2), e, n, k, _ptr(out), _stream(w))
+    return out
+
+
+@_fake("weight8_kmajor")
+def _(w):
+    k = w.size(-1)
+    shape = (k // 128, w.size(0), 128) if w.dim() == 2 else (w.size(0), k // 128, w.size(1), 128)
+    return w.new_empty(shape)
+
+
+@_define("fp8_w8a8_block_gemm_kmajor(Tensor qa, Tensor sa, Tensor w_kmajor, Tensor sw, int cfg=-1) -> Tensor")
+def fp8_w8a8_block_gemm_kmajor(qa, sa, w_kmajor, sw, cfg=-1):
+    """fp8_w8a8_block_gemm on weights already in K-block-major order
+    (weight8_kmajor): the same result, bit for bit."""
+    _rowmajor(qa, "qa")
+    _check(qa.dtype == torch.float8_e4m3fn and w_kmajor.dtype == torch.float8_e4m3fn, "qa and w must be float8_e4m3fn")
+    _check(w_kmajor.dim() == 3 and w_kmajor.size(2) == 128 and w_kmajor.is_contiguous(),
+           "w_kmajor must be contiguous [K/128, N, 128]")
+    m, k = qa.shape
+    n = w_kmajor.size(1)
+    _check(w_kmajor.size(0) * 128 == k, f"Activation K ({k}) must match weight K ({w_kmajor.size(0) * 128})")
+    _check(sa.dtype == torch.float32 and tuple(sa.shape) == (m, k // 128) and sa.stride(1) == 1,
+           "sa must be float32 [M, K/128]")
+    _check(sw.dtype == torch.float32 and tuple(sw.shape) == ((n + 127) // 128, k // 128) and sw.stride(1) == 1,
+           "sw must be float32 [ceil(N/128), K/128]")
+    out = torch.empty((m, n), dtype=torch.bfloat16, device=qa.device)
+    _lib.call("strix_fp8_w8a8_block_gemm_kmajor", _ptr(qa), qa.stride(0), _ptr(sa), sa.stride(0), _ptr(w_kmajor),
+              _ptr(sw), sw.stride(0), _ptr(out), n, _lib.BF16, m, n, k, int(cfg), _stream(qa))
+    return out
+
+
+@_fake("fp8_w8a8_block_gemm_kmajor")
+def _(qa, sa, w_kmajor, sw, cfg=-1):
+    return qa.new_empty((qa.size(0), w_kmajor.size(1)), dtype=torch.bfloat16)
+
+
 # ----------------------------------------------------------------- MoE
 def _moe_common(c, sorted_ids, expert_ids, num_post_padded, topk_weights, block_m):
     _check(sorted_ids.dtype == torch.int32 and expert_ids.dtype == torch.int32 and num_post_padded.dtype == torch.int32,
@@ -289,8 +340,16 @@ def _moe_common(c, sorted_ids, expert_ids, num_post_padded, topk_weights, block_
 )
 def moe_gemm_fp8_w8a8(c, qa, sa, b, scales, sorted_ids, expert_ids, num_post_padded, topk_weights, top_k, block_m,
                       block_n, silu_mul=False, activation="silu"):
-    _check(b.dim() == 3 and b.dtype == torch.float8_e4m3fn and b.stride(2) == 1, "b must be float8_e4m3fn [E, N, K]")
-    e, n, k = b.shape
+    # b: row-major [E, N, K], or K-block-major [E, K/128, N, 128] (weight8_kmajor).
+    kmajor = b.dim() == 4
+    if kmajor:
+        _check(b.dtype == torch.float8_e4m3fn and b.size(3) == 128 and b.is_contiguous(),
+               "K-block-major b must be contiguous float8_e4m3fn [E, K/128, N, 128]")
+        e, n, k = b.size(0), b.size(2), b.size(1) * 128
+    else:
+        _check(b.dim() == 3 and b.dtype == torch.float8_e4m3fn and b.stride(2) == 1,
+               "b must be float8_e4m3fn [E, N, K] or [E, K/128, N, 128]")
+        e, n, k = b.shape
     _rowmajor(qa, "qa")
     _check(qa.dtype == torch.float8_e4m3fn and qa.size(1) == k, "qa must be float8_e4m3fn [rows, K]")
     _check(sa.dtype == torch.float32 and sa.dim() == 2 and sa.size(1) == k // 128 and sa.stride(1) == 1,
@@ -300,6 +359,13 @@ def moe_gemm_fp8_w8a8(c, qa, sa, b, scales, sorted_ids, expert_ids, num_post_pad
     _check(c.dim() == 2 and c.stride(1) == 1 and c.dtype in (torch.bfloat16, torch.float16), "c must be bf16/fp16 2-D")
     _check(n % block_n == 0, f"N={n} is not a multiple of block_n={block_n}")
     _moe_common(c, sorted_ids, expert_ids, num_post_padded, topk_weights, block_m)
+    if kmajor:
+        _lib.call("strix_moe_gemm_fp8_w8a8_kmajor", _ptr(c), c.stride(0), _out_code(c.dtype), _ptr(qa), qa.stride(0),
+                  _ptr(sa), sa.stride(0), _ptr(b), _ptr(scales), scales.stride(0), scales.stride(1),
+                  _ptr(sorted_ids), sorted_ids.numel(), _ptr(expert_ids), expert_ids.numel(), _ptr(num_post_padded),
+                  _ptr(topk_weights), c.size(0), top_k, block_m, int(bool(silu_mul)), _activation(activation), n, k,
+                  _stream(c))
+        return
     _lib.call("strix_moe_gemm_fp8_w8a8", _ptr(c), c.stride(0), _out_code(c.dtype), _ptr(qa), qa.stride(0), _ptr(sa),
               sa.stride(0), _ptr(b), b.stride(0), b.stride(1), _ptr(scales), scales.stride(0), scales.stride(1),
               _ptr(sorted_ids), sorted_ids.numel(), _ptr(expert_ids), expert_ids.numel(), _ptr(num_post_padded),

@@ -91,3 +91,37 @@ def test_rejects_bad_k():
     x = torch.zeros(4, 96, dtype=torch.float8_e4m3fn, device=DEV)
     with pytest.raises(RuntimeError, match="K must be a multiple of 128"):
         torch.ops.strix.fp8_w8a8_block_gemm(x, torch.ones(4, 1, device=DEV), x, torch.ones(1, 1, device=DEV))
+
+
+def test_weight8_kmajor_layout():
+    # [E, N, K] -> [E, K/128, N, 128] is a pure permutation of bytes.
+    g = torch.Generator().manual_seed(7)
+    w = torch.randint(-128, 128, (3, 200, 384), generator=g, dtype=torch.int8)
+    got = torch.ops.strix.weight8_kmajor(w.to(DEV)).cpu()
+    want = w.view(3, 200, 3, 128).permute(0, 2, 1, 3).contiguous()
+    assert torch.equal(got, want)
+    got2 = torch.ops.strix.weight8_kmajor(w[1].to(DEV)).cpu()
+    assert torch.equal(got2, want[1])
+
+
+@pytest.mark.parametrize("m", [1, 4, 16, 17, 32, 33, 100, 256, 520, 4096])
+@pytest.mark.parametrize("n,k", [(17408, 5120), (300, 1024), (520, 4096)])
+def test_kmajor_gemm_matches_rowmajor(m, n, k):
+    # Same kernels, other weight addressing: the outputs agree bit for bit.
+    if m == 4096 and n != 17408:
+        pytest.skip("one full-size prefill shape is enough")
+    d = workloads.c2_fp8(seed=40 + m, m=m, n=n, k=k, device=DEV)
+    qa, sa = torch.ops.strix.fp8_quant_group128(d["x"])
+    want = torch.ops.strix.fp8_w8a8_block_gemm(qa, sa, d["w"], d["sw"])
+    wk = torch.ops.strix.weight8_kmajor(d["w"])
+    got = torch.ops.strix.fp8_w8a8_block_gemm_kmajor(qa, sa, wk, d["sw"])
+    assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("cfg", range(12))
+def test_kmajor_every_cfg(cfg):
+    d = workloads.c2_fp8(seed=60 + cfg, m=70, n=520, k=1024, device=DEV)
+    qa, sa = torch.ops.strix.fp8_quant_group128(d["x"])
+    want = torch.ops.strix.fp8_w8a8_block_gemm_cfg(qa, sa, d["w"], d["sw"], cfg)
+    got = torch.ops.strix.fp8_w8a8_block_gemm_kmajor(qa, sa, torch.ops.strix.weight8_kmajor(d["w"]), d["sw"], cfg)
+    assert torch.equal(got, want)

@@ -195,3 +195,17 @@ def test_config3_fused_moe(t, c3_weights):
                            lambda e: oracle.fp8_block_dequant(d["w2"][e], d["w2_s"][e]),
                            act_quant="fp8", tokens=rows)
     assert peak_rel_err(out.cpu()[rows], ref) <= TOL
+
+
+@pytest.mark.parametrize("t", [1, 64, 700])
+def test_fused_moe_kmajor_weights_bit_identical(t):
+    # K-block-major expert weights (weight8_kmajor) through the whole chain:
+    # the same bits as row-major, for the decode and the tiled kernels.
+    c3 = workloads.c3_fp8_moe(seed=5, t=1, device=DEV)
+    logits = torch.randn(t, 128, generator=torch.Generator().manual_seed(t)).to(DEV)
+    x = torch.randn(t, 2048, generator=torch.Generator().manual_seed(t + 1)).to(torch.bfloat16).to(DEV)
+    want = functional.fused_moe_fp8_w8a8(x, logits, c3["w13"], c3["w13_s"], c3["w2"], c3["w2_s"], 8)
+    w13k, w2k = torch.ops.strix.weight8_kmajor(c3["w13"]), torch.ops.strix.weight8_kmajor(c3["w2"])
+    assert w13k.shape == (128, 16, 1536, 128) and w2k.shape == (128, 6, 2048, 128)
+    got = functional.fused_moe_fp8_w8a8(x, logits, w13k, c3["w13_s"], w2k, c3["w2_s"], 8)
+    assert torch.equal(got, want)

@@ -55,6 +55,10 @@ def test_fp8_block_linear_w8a8(m):
     out = fp8._apply_impl(x.to(DEV), wd, bsd, None, True).cpu()
     qa, sa = oracle.fp8_quant_group128(x)
     assert peak_rel_err(out, oracle.fp8_block_gemm(qa, sa, w, bs)) <= TOL
+    # The plugin's load transform re-lays the weights K-block-major: same bits.
+    wk, bsk = fp8.prepare_block(w.to(DEV), bs.to(DEV), kmajor=True)
+    assert wk.shape == (k // 128, n, 128)
+    assert torch.equal(fp8._apply_impl(x.to(DEV), wk, bsk, None, True).cpu(), out)
 
 
 @pytest.mark.parametrize("m", [1, 8, fp8.W8A16_DEQUANT_MIN_M - 1, fp8.W8A16_DEQUANT_MIN_M, 300])

@@ -41,6 +41,8 @@ _OUT = {
     "w8a8_scaled_mm": lambda q, s, w, sw: torch.zeros(q.size(0), w.size(0), dtype=torch.bfloat16),
     "fp8_quant_group128": lambda x: (torch.zeros(x.shape), torch.ones(x.size(0), x.size(1) // 128)),
     "fp8_w8a8_block_gemm": lambda q, s, w, sw: torch.zeros(q.size(0), w.size(0), dtype=torch.bfloat16),
+    "fp8_w8a8_block_gemm_kmajor": lambda q, s, w, sw: torch.zeros(q.size(0), w.size(1), dtype=torch.bfloat16),
+    "weight8_kmajor": lambda w: w.view(w.size(0), -1, 128).permute(1, 0, 2).contiguous(),
     "fp8_dequant": lambda w, s: torch.zeros(w.shape, dtype=torch.bfloat16),
     "fp8_wmma_gemm": lambda w, x, s: torch.zeros(x.size(0), w.size(0), dtype=torch.bfloat16),
     "mxfp4_gemv": lambda x, w, s: torch.zeros(x.size(0), w.size(0), dtype=torch.bfloat16),
@@ -256,6 +258,16 @@ def test_int8_dispatch_quantizes_per_token(rec):
 def test_fp8_block_dispatch_is_w8a8_at_every_m(rec, m):
     fp8._apply_impl(torch.zeros(m, 256, dtype=torch.bfloat16), torch.zeros(128, 256), torch.ones(1, 2), None, True)
     assert rec.calls == ["fp8_quant_group128", "fp8_w8a8_block_gemm"]
+
+
+def test_fp8_block_kmajor_weights(rec):
+    # The W8A8 load transform re-lays the weights K-block-major; the forward
+    # then calls the K-major GEMM and the output keeps N columns.
+    w = torch.zeros(128, 256)
+    wk, _ = fp8.prepare_block(w.to(torch.float8_e4m3fn), torch.ones(1, 2), kmajor=True)
+    assert rec.calls == ["weight8_kmajor"] and wk.shape == (2, 128, 128) and fp8.out_features(wk) == 128
+    out = fp8._apply_impl(torch.zeros(3, 256, dtype=torch.bfloat16), wk, torch.ones(1, 2), None, True)
+    assert rec.calls[1:] == ["fp8_quant_group128", "fp8_w8a8_block_gemm_kmajor"] and out.shape == (3, 128)
 
 
 @pytest.mark.parametrize("m,expect", [(1, "fp8_wmma_gemm"), (fp8.W8A16_DEQUANT_MIN_M - 1, "fp8_wmma_gemm"),
