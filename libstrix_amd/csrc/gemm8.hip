@@ -1082,7 +1082,10 @@ int moe_dispatch(const G8& p, int block_m, int num_blocks, hipStream_t st, const
   constexpr int NTS = (EPI == kEpiGated) ? 2 : 1;
   switch (block_m) {
     // No K split here: measured slower at T=1 (29 -> 32 us for config 3).
-    case 16: return launch_ring<KIND, NTS, true, EPI, ACT, 5, false, 1>(p, num_blocks, st, op);
+    // Two 16-row weight subtiles per wave for both GEMMs: the short-K down
+    // projection keeps twice the bytes in flight per wave (config 3 T=64
+    // 145 -> 140 us).
+    case 16: return launch_ring<KIND, 2, true, EPI, ACT, 5, false, 1>(p, num_blocks, st, op);
     case 32: return launch_stream<KIND, NTS, 2, 2, true, EPI, ACT, 4, false>(p, num_blocks, st, op);
     case 64: return launch_tiled<KIND, 64, 128, 1, 4, 4, true, EPI, ACT, false>(p, num_blocks, st, op);
     case 128: return launch_tiled<KIND, 128, 128, 2, 2, 4, true, EPI, ACT, false>(p, num_blocks, st, op);
