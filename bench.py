@@ -45,10 +45,20 @@ class Timer:
     def __init__(self, torch):
         self.torch = torch
 
-    def __call__(self, fn, iters: int, warmup: int = 10) -> float:
+    def __call__(self, fn, iters: int, warmup: int = 10, warm_s: float = 0.05) -> float:
+        # Warm up for `warmup` calls and at least `warm_s` seconds: under a
+        # sustained MFMA load the MI355X first drops its clock and then climbs
+        # back over some tens of milliseconds (the 256x256 FP8 GEMM runs ~400 us
+        # a few calls in and ~300 us after ~100 calls), so a short warm-up
+        # times the transient instead of the steady state.
         torch = self.torch
-        for _ in range(warmup):
-            fn(0)
+        t_end = time.perf_counter() + warm_s
+        n = 0
+        while n < warmup or time.perf_counter() < t_end:
+            fn(n)
+            n += 1
+            if n % 8 == 0:
+                torch.cuda.synchronize()
         torch.cuda.synchronize()
         a = torch.cuda.Event(enable_timing=True)
         b = torch.cuda.Event(enable_timing=True)
@@ -161,7 +171,13 @@ def point_c2(torch, S, timer, m, weights):
         w, sw = sets[i % len(sets)]
         return S.fp8_w8a8_block_gemm(q, s, w, sw)
 
-    us_k = timer(gemm, iters=max(20, 3 * len(sets)))
+    # Up to M=256 an eager loop is bound by the host's per-call overhead
+    # (Python checks, ctypes), not the GPU: the kernel time comes from graph
+    # replay, one GEMM per cold weight set, as a serving loop sees it.
+    if m <= 256:
+        us_k = graph_us(torch, [lambda w=w, sw=sw: S.fp8_w8a8_block_gemm(q, s, w, sw) for (w, sw) in sets])
+    else:
+        us_k = timer(gemm, iters=max(20, 3 * len(sets)))
     us_op = timer(lambda i: (lambda qq: S.fp8_w8a8_block_gemm(qq[0], qq[1], *sets[i % len(sets)]))(
         S.fp8_quant_group128(x)), iters=max(20, 3 * len(sets)))
     flops = 2.0 * m * n * k
@@ -172,7 +188,10 @@ def point_c2(torch, S, timer, m, weights):
            "frac_hbm": round(by / us_k / 1e3 / PEAK_HBM_GBS, 4), "cold_weight_sets": len(sets)}
     # The plugin's layout: the same weights K-block-major (weight8_kmajor), same bits.
     ksets = [(S.weight8_kmajor(w), sw) for (w, sw) in sets]
-    us_kk = timer(lambda i: S.fp8_w8a8_block_gemm_kmajor(q, s, *ksets[i % len(ksets)]), iters=max(20, 3 * len(sets)))
+    if m <= 256:
+        us_kk = graph_us(torch, [lambda w=w, sw=sw: S.fp8_w8a8_block_gemm_kmajor(q, s, w, sw) for (w, sw) in ksets])
+    else:
+        us_kk = timer(lambda i: S.fp8_w8a8_block_gemm_kmajor(q, s, *ksets[i % len(ksets)]), iters=20)
     res.update({"kmajor_gemm_us": round(us_kk, 2), "kmajor_tflops": round(flops / us_kk / 1e6, 1),
                 "kmajor_frac_hbm": round(by / us_kk / 1e3 / PEAK_HBM_GBS, 4)})
     if m <= 16:
@@ -196,16 +215,13 @@ def point_c1(torch, S, timer):
     x = d["x"]
     q, s = S.int8_quant_per_token(x)
 
-    def gemm(i):
-        w, sw = sets[i % len(sets)]
-        return S.w8a8_scaled_mm(q, s, w, sw)
-
     def op(i):
         w, sw = sets[i % len(sets)]
         qq, ss = S.int8_quant_per_token(x)
         return S.w8a8_scaled_mm(qq, ss, w, sw)
 
-    us_k = timer(gemm, iters=3 * len(sets))
+    # Kernel time from graph replay (an eager loop of a 10 us kernel measures the host).
+    us_k = graph_us(torch, [lambda w=w, sw=sw: S.w8a8_scaled_mm(q, s, w, sw) for (w, sw) in sets])
     us_op = timer(op, iters=3 * len(sets))
     by = n * k + n * 4 + m * k * 2 + m * n * 2
     ops = 2.0 * m * n * k
@@ -304,8 +320,10 @@ def traffic_from_profile():
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=20)
+    # Defaults: ~60 ms of warm-up reaches the steady clock of a sustained MFMA
+    # load (see Timer); the timed 100 steps take ~35 ms.
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-points", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
