@@ -1040,21 +1040,45 @@ int launch_dense_256(const G8& p, hipStream_t st, const char* op) {
   return launch_tiled<KIND, 256, 256, 4, 2, 2, false, EPI, kActSilu, WX128>(p, 0, st, op);
 }
 
+// Automatic config of the dense 8-bit GEMM: up to 32 rows the weight ring;
+// above, the cheapest of four priced candidates (the wider tile on a tie).
+//  - ring: one weight stream per 32 token rows, N*K bytes at 5 TB/s each,
+//    plus 3 us;
+//  - 128x128, 128x256, 256x256 tiles: (rounds of tiles over the CUs) x (one
+//    tile at the shape's per-CU rate + 4 us), the rates measured on MI355X
+//    over one full round of FP8-block tiles (5.9, 7.6, 9.1 TFLOP/s per CU);
+//    256x256 adds its 128x128 column strip when it uses one.
+// Fitted on a sweep of six shapes (N x K from 2048 x 7168 to 17408 x 5120,
+// M 48..2048), this picks the fastest config, or one within 5 % of it, on
+// every point; the fixed rule it replaces lost up to 2x (N=5120 K=17408:
+// M=64 96 -> 46 us, M=256 149 -> 97 us; N=17408 K=5120 M=512 101 -> 74 us).
+// int8 group weights keep the fixed rule (their 128x256 config is 128x128).
+inline int dense_auto_cfg(int64_t M, int64_t n_out, int64_t K, bool group) {
+  if (M <= 32) return 0;
+  const int64_t cus = cu_count();
+  auto tiles = [&](int64_t bm, int64_t bn) { return ((M + bm - 1) / bm) * ((n_out + bn - 1) / bn); };
+  auto rounds = [&](int64_t t) { return (double)((t + cus - 1) / cus); };
+  const int64_t t256 = tiles(256, 256);
+  if (group) return M <= 128 ? 3 : (t256 >= cus ? 5 : 6);
+  const double flop = 2.0 * (double)K;  // per output element of a tile
+  const double T3 = 128.0 * 128.0 * flop / 5.9e6 + 4.0;  // us
+  const double T6 = 128.0 * 256.0 * flop / 7.6e6 + 4.0;
+  const double T5 = 256.0 * 256.0 * flop / 9.1e6 + 4.0;
+  const double e0 = (double)((M + 31) / 32) * (double)n_out * (double)K / 5e6 + 3.0;
+  const double e3 = rounds(tiles(128, 128)) * T3, e6 = rounds(tiles(128, 256)) * T6;
+  const int64_t r5 = t256 / cus, rem = t256 % cus;
+  const double e5 = (r5 >= 1 && rem > 0 && 2 * rem <= cus) ? (double)r5 * T5 + rounds(4 * rem) * T3
+                                                          : rounds(t256) * T5;
+  if (e5 <= e6 && e5 <= e3 && e5 <= e0) return 5;
+  if (e6 <= e3 && e6 <= e0) return 6;
+  return e3 <= e0 ? 3 : 0;
+}
+
 // Dense dispatch by M. cfg >= 0 pins one tile config (tile sweeps).
 template <int KIND, int EPI, bool WX128>
 int dense_dispatch(const G8& p, hipStream_t st, const char* op, int cfg) {
   const int M = p.M;
-  if (cfg < 0) {
-    // Decode streams the weights through a per-wave LDS ring. Above that the
-    // tile shape is the largest whose tile count still fills the chip: 256x256
-    // once it covers every CU, 128x256 (three stages) below that, and 128x128
-    // up to 128 rows, where the wider tiles leave most CUs idle.
-    const int64_t t256 = (int64_t)((M + 255) / 256) * ((p.n_out + 255) / 256);
-    if (M <= 32) cfg = 0;
-    else if (M <= 128) cfg = 3;
-    else if (t256 >= cu_count()) cfg = 5;
-    else cfg = 6;
-  }
+  if (cfg < 0) cfg = dense_auto_cfg(M, p.n_out, p.K, KIND == kI8Group);
   switch (cfg) {
     case 0: return launch_ring<KIND, 1, false, EPI, kActSilu, 5, WX128, 1, true, true>(p, (M + 15) / 16, st, op);
     case 1: return launch_stream<KIND, 1, 2, 4, false, EPI, kActSilu, 4, WX128>(p, (M + 31) / 32, st, op);
