@@ -19,6 +19,8 @@
 //   tiled8:  BM x BN block tile, direct global->LDS copies (no register
 //            staging) into a fragment-native layout, two LDS stages of 128 K,
 //            conflict-free ds_read_b128 fragment reads. Prefill.
+#include <cmath>
+
 #include "capi_internal.h"
 #include "gemm_common.h"
 #include "strix_common.h"
@@ -988,6 +990,47 @@ int launch_ring(const G8& p, int grid_y, hipStream_t st, const char* op) {
   return check_launch(op);
 }
 
+// Dense decode ring (the automatic config up to 32 rows and wherever the
+// weights stream): the ring depth and K split set the weight bytes in flight
+// and how compact the window of concurrent reads is. A sweep on MI355X
+// (K-block-major FP8, N x K from 2048 x 7168 to 17408 x 5120, M 1..32) found
+// a three-slot ring with the K split sized to about five waves per CU best or
+// near it almost everywhere (N=17408 K=5120: M=16 22.0 -> 18.5 us, M=32 28.6
+// -> 26.6; N=5120 K=5120 M=32 14.4 -> 9.4; N=5120 K=17408 M=1 21.7 -> 19.1),
+// except two token copies with long K (N=5120 K=17408 at M=16: 27 us unsplit
+// with five slots, 40 with three) and int8 tokens with two copies (config 1,
+// M=32: 10.7 vs 11.1 us), which keep the five-slot ring and its split rule.
+template <int KIND, int EPI, bool WX128>
+int launch_ring_dense(const G8& p, hipStream_t st, const char* op) {
+  const int64_t cus = cu_count();
+  const int grid_x = (p.n_out + 15) / 16;
+  const bool t32 = p.M > 16 && (int64_t)grid_x * ((p.M + 31) / 32) >= 4 * cus;
+  const int tq = p.M <= 8 ? 1 : (t32 ? 4 : 2);
+  const int nks = p.K >> 7;
+  if (tq == 2 && (KIND == kI8Token || nks > 64))
+    return launch_ring<KIND, 1, false, EPI, kActSilu, 5, WX128, 1, true, true>(p, (p.M + 15) / 16, st, op);
+  const int grid_y = tq == 4 ? (p.M + 31) / 32 : (p.M + 15) / 16;
+  const double per_cu = (double)grid_x * grid_y / (double)cus;  // waves per CU without a split
+  int ks = 1;
+  for (int c : {2, 4})
+    if (nks >= 4 * c && std::fabs(per_cu * c - 5.0) < std::fabs(per_cu * ks - 5.0)) ks = c;
+  auto go = [&](auto tq_tag, auto ks_tag) {
+    constexpr int TQ_ = decltype(tq_tag)::value;
+    constexpr int KS_ = decltype(ks_tag)::value;
+    hipLaunchKernelGGL((ring8_kernel<KIND, 1, false, EPI, kActSilu, 3, WX128, TQ_, 1, KS_>), dim3(grid_x, grid_y),
+                       dim3(64 * KS_), 0, st, p);
+  };
+  auto with_ks = [&](auto tq_tag) {
+    if (ks == 4) go(tq_tag, std::integral_constant<int, 4>{});
+    else if (ks == 2) go(tq_tag, std::integral_constant<int, 2>{});
+    else go(tq_tag, std::integral_constant<int, 1>{});
+  };
+  if (tq == 1) with_ks(std::integral_constant<int, 1>{});
+  else if (tq == 2) with_ks(std::integral_constant<int, 2>{});
+  else with_ks(std::integral_constant<int, 4>{});
+  return check_launch(op);
+}
+
 template <int KIND, int BM, int BN, int WM, int WN, int STAGES, bool MOE, int EPI, int ACT, bool WX128>
 int launch_tiled(const G8& p, int grid_y_moe, hipStream_t st, const char* op) {
   constexpr int COLS = (EPI == kEpiGated) ? BN / 2 : BN;
@@ -1080,7 +1123,7 @@ int dense_dispatch(const G8& p, hipStream_t st, const char* op, int cfg) {
   const int M = p.M;
   if (cfg < 0) cfg = dense_auto_cfg(M, p.n_out, p.K, KIND == kI8Group);
   switch (cfg) {
-    case 0: return launch_ring<KIND, 1, false, EPI, kActSilu, 5, WX128, 1, true, true>(p, (M + 15) / 16, st, op);
+    case 0: return launch_ring_dense<KIND, EPI, WX128>(p, st, op);
     case 1: return launch_stream<KIND, 1, 2, 4, false, EPI, kActSilu, 4, WX128>(p, (M + 31) / 32, st, op);
     case 2: return launch_stream<KIND, 1, 4, 4, false, EPI, kActSilu, 2, WX128>(p, (M + 63) / 64, st, op);
     case 3: return launch_tiled<KIND, 128, 128, 2, 2, 4, false, EPI, kActSilu, WX128>(p, 0, st, op);
