@@ -19,6 +19,7 @@
 //   tiled8:  BM x BN block tile, direct global->LDS copies (no register
 //            staging) into a fragment-native layout, two LDS stages of 128 K,
 //            conflict-free ds_read_b128 fragment reads. Prefill.
+#include <algorithm>
 #include <cmath>
 
 #include "capi_internal.h"
@@ -1151,8 +1152,16 @@ int moe_dispatch(const G8& p, int block_m, int num_blocks, hipStream_t st, const
     // No K split here: measured slower at T=1 (29 -> 32 us for config 3).
     // Two 16-row weight subtiles per wave for both GEMMs: the short-K down
     // projection keeps twice the bytes in flight per wave (config 3 T=64
-    // 145 -> 140 us).
-    case 16: return launch_ring<KIND, 2, true, EPI, ACT, 5, false, 1>(p, num_blocks, st, op);
+    // 145 -> 140 us). Three ring slots once the live blocks (at most one per
+    // routed slot) give four waves per CU, five below (config 3: T=64 140 ->
+    // 134 us with three, T=1 31 -> 33 us).
+    case 16: {
+      constexpr int COLS = (EPI == kEpiGated) ? 16 : 32;  // output columns per wave
+      const int64_t live = std::min<int64_t>(num_blocks, p.num_slots);
+      if ((int64_t)((p.n_out + COLS - 1) / COLS) * live >= 4LL * cu_count())
+        return launch_ring<KIND, 2, true, EPI, ACT, 3, false, 1>(p, num_blocks, st, op);
+      return launch_ring<KIND, 2, true, EPI, ACT, 5, false, 1>(p, num_blocks, st, op);
+    }
     case 32: return launch_stream<KIND, NTS, 2, 2, true, EPI, ACT, 4, false>(p, num_blocks, st, op);
     case 64: return launch_tiled<KIND, 64, 128, 1, 4, 4, true, EPI, ACT, false>(p, num_blocks, st, op);
     case 128: return launch_tiled<KIND, 128, 128, 2, 2, 4, true, EPI, ACT, false>(p, num_blocks, st, op);
