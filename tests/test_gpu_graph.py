@@ -62,3 +62,18 @@ def test_fused_moe_mxfp4_graph():
     x = torch.randn(2, 2880, generator=torch.Generator().manual_seed(6)).to(torch.bfloat16).to(DEV)
     fn = lambda: functional.fused_moe_mxfp4(x, logits, c4["w13"], c4["w13_s"], c4["w2"], c4["w2_s"], 4)
     _replays_match(fn, fn().clone())
+
+
+@pytest.mark.parametrize("t", [1, 64])
+def test_plugin_fp8_experts_graph(t):
+    # The plugin's FP8 expert chain (quantize, align, both GEMMs, combine)
+    # captured as vLLM captures its decode step: every replay equals eager.
+    from libstrix_amd.vllm_plugin import moe
+
+    c3 = workloads.c3_fp8_moe(seed=7, t=1, device=DEV)
+    g = torch.Generator().manual_seed(t + 9)
+    ids = torch.stack([torch.randperm(128, generator=g)[:8] for _ in range(t)]).to(torch.int32).to(DEV)
+    tw = torch.rand(t, 8, generator=g).to(DEV)
+    x = torch.randn(t, 2048, generator=g).to(torch.bfloat16).to(DEV)
+    fn = lambda: moe.fp8_experts(None, x, c3["w13"], c3["w2"], c3["w13_s"], c3["w2_s"], tw, ids, "silu")
+    _replays_match(fn, fn().clone())
