@@ -73,7 +73,7 @@ int strix_fp8_quant_group128(const void* x, int x_dtype, int64_t ldx, uint8_t* q
 /* ------------------------------------------------------------------ 8-bit GEMMs
  * FP8-block W8A8: out[M,N] = sum_kb sa[m,kb] sw[n/128,kb] (qa[m,kb] . qw[n,kb]).
  * qa e4m3 [M, lda], sa fp32 [M, sa_ld], w e4m3 [N, ldw], sw fp32 [ceil(N/128), sw_ld].
- * cfg -1 picks the tile by M; 0..6 pins one (tile sweeps, cf. fp8_wmma_gemm_cfg,
+ * cfg -1 picks the tile by shape; 0..12 pins one (tile sweeps, cf. fp8_wmma_gemm_cfg,
  * csrc/torch_ops.cpp:253). Replaces fp8_wmma_gemm's dense FP8 role
  * (csrc/gemm/fp8_wmma_gemm.hip:253-322) with native e4m3 MFMA. */
 int strix_fp8_w8a8_block_gemm(const uint8_t* qa, int64_t lda, const float* sa, int64_t sa_ld,

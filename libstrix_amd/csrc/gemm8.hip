@@ -21,6 +21,7 @@
 //            conflict-free ds_read_b128 fragment reads. Prefill.
 #include <algorithm>
 #include <cmath>
+#include <utility>
 
 #include "capi_internal.h"
 #include "gemm_common.h"
@@ -1088,10 +1089,10 @@ int launch_dense_256(const G8& p, hipStream_t st, const char* op) {
 // above, the cheapest of four priced candidates (the wider tile on a tie).
 //  - ring: one weight stream per 32 token rows, N*K bytes at 5 TB/s each,
 //    plus 3 us;
-//  - 128x128, 128x256, 256x256 tiles: (rounds of tiles over the CUs) x (one
-//    tile at the shape's per-CU rate + 4 us), the rates measured on MI355X
-//    over one full round of FP8-block tiles (5.9, 7.6, 9.1 TFLOP/s per CU);
-//    256x256 adds its 128x128 column strip when it uses one.
+//  - 128x128, 128x160, 128x256, 256x256 tiles: (rounds of tiles over the
+//    CUs) x (one tile at the shape's per-CU rate + 4 us), the rates measured
+//    on MI355X over one full round of FP8-block tiles (5.9, 5.6, 7.6, 9.1
+//    TFLOP/s per CU); 256x256 adds its 128x128 column strip when it uses one.
 // Fitted on a sweep of six shapes (N x K from 2048 x 7168 to 17408 x 5120,
 // M 48..2048), this picks the fastest config, or one within 5 % of it, on
 // every point; the fixed rule it replaces lost up to 2x (N=5120 K=17408:
@@ -1108,14 +1109,20 @@ inline int dense_auto_cfg(int64_t M, int64_t n_out, int64_t K, bool group) {
   const double T3 = 128.0 * 128.0 * flop / 5.9e6 + 4.0;  // us
   const double T6 = 128.0 * 256.0 * flop / 7.6e6 + 4.0;
   const double T5 = 256.0 * 256.0 * flop / 9.1e6 + 4.0;
+  const double T12 = 128.0 * 160.0 * flop / 5.6e6 + 4.0;
   const double e0 = (double)((M + 31) / 32) * (double)n_out * (double)K / 5e6 + 3.0;
   const double e3 = rounds(tiles(128, 128)) * T3, e6 = rounds(tiles(128, 256)) * T6;
+  const double e12 = rounds(tiles(128, 160)) * T12;
   const int64_t r5 = t256 / cus, rem = t256 % cus;
   const double e5 = (r5 >= 1 && rem > 0 && 2 * rem <= cus) ? (double)r5 * T5 + rounds(4 * rem) * T3
                                                           : rounds(t256) * T5;
-  if (e5 <= e6 && e5 <= e3 && e5 <= e0) return 5;
-  if (e6 <= e3 && e6 <= e0) return 6;
-  return e3 <= e0 ? 3 : 0;
+  // Candidates from the widest tile down; the first strictly cheaper wins.
+  int best = 5;
+  double eb = e5;
+  const std::pair<int, double> rest[] = {{6, e6}, {12, e12}, {3, e3}, {0, e0}};
+  for (const auto& c : rest)
+    if (c.second < eb) { best = c.first; eb = c.second; }
+  return best;
 }
 
 // Dense dispatch by M. cfg >= 0 pins one tile config (tile sweeps).
@@ -1140,7 +1147,13 @@ int dense_dispatch(const G8& p, hipStream_t st, const char* op, int cfg) {
     case 9: return launch_ring<KIND, 1, false, EPI, kActSilu, 7, WX128, KIND == kI8Group ? 1 : 4>(p, (M + 15) / 16, st, op);
     case 10: return launch_ring<KIND, 1, false, EPI, kActSilu, 7, WX128, 1>(p, (M + 15) / 16, st, op);
     case 11: return launch_ring<KIND, 1, false, EPI, kActSilu, 6, WX128, KIND == kI8Group ? 1 : 4>(p, (M + 15) / 16, st, op);
-    default: return set_error(STRIX_ERR_INVALID, "%s: cfg must be in 0..11, got %d", op, cfg);
+    // 128x160: a round that 128x256 fills only half, filled to 85 % (17408
+    // columns in 109 tiles per 128 rows: config 2 at M=256 54.4 -> 42.4 us).
+    // int8 group scales need 64-row multiples: 128x128 there.
+    case 12:
+      if constexpr (KIND == kI8Group) return launch_tiled<KIND, 128, 128, 2, 2, 4, false, EPI, kActSilu, WX128>(p, 0, st, op);
+      else return launch_tiled<KIND, 128, 160, 2, 2, 3, false, EPI, kActSilu, WX128>(p, 0, st, op);
+    default: return set_error(STRIX_ERR_INVALID, "%s: cfg must be in 0..12, got %d", op, cfg);
   }
 }
 

@@ -137,7 +137,7 @@ KERNELS: list[Kernel] = [
     Kernel(
         "w8a8_scaled_mm_cfg",
         "w8a8_int8_tile_sweep",
-        "w8a8_scaled_mm pinned to one tile config (0..11), for tile sweeps",
+        "w8a8_scaled_mm pinned to one tile config (0..12), for tile sweeps",
         {"weight_dtype": "int8", "granularity": "token"},
     ),
     Kernel(
@@ -150,7 +150,7 @@ KERNELS: list[Kernel] = [
     Kernel(
         "w8a8_wmma_gemm_cfg",
         "w8a8_tile_sweep",
-        "the W8A8 group GEMM pinned to one tile config (0..11), same math and activation quantize",
+        "the W8A8 group GEMM pinned to one tile config (0..12), same math and activation quantize",
         {"weight_bits": 8, "rows": Range(lo=1), "dtype": ("bf16", "fp16")},
         {"cfgs": "0 stream 16 | 1 stream 32 | 2 stream 64 | 3 tiled 128x128 | 4 tiled 256x64 | "
                  "5 tiled 256x256 | 6 tiled 128x256"},
@@ -169,7 +169,7 @@ KERNELS: list[Kernel] = [
     Kernel(
         "fp8_w8a8_block_gemm_cfg",
         "fp8_w8a8_tile_sweep",
-        "fp8_w8a8_block_gemm pinned to one tile config (0..11)",
+        "fp8_w8a8_block_gemm pinned to one tile config (0..12)",
         {"weight_dtype": "fp8_e4m3", "activation_dtype": "fp8_e4m3", "group_size": 128},
     ),
     Kernel(

@@ -46,7 +46,7 @@ def test_shapes_and_ragged_n(m, n, k):
     assert peak_rel_err(out, oracle.fp8_block_gemm(qa, sa, d["w"], d["sw"])) <= TOL
 
 
-@pytest.mark.parametrize("cfg", range(12))
+@pytest.mark.parametrize("cfg", range(13))
 def test_every_cfg(cfg):
     d = workloads.c2_fp8(seed=cfg, m=70, n=640, k=1536)
     qa, sa = oracle.fp8_quant_group128(d["x"])
@@ -118,7 +118,7 @@ def test_kmajor_gemm_matches_rowmajor(m, n, k):
     assert torch.equal(got, want)
 
 
-@pytest.mark.parametrize("cfg", range(12))
+@pytest.mark.parametrize("cfg", range(13))
 def test_kmajor_every_cfg(cfg):
     d = workloads.c2_fp8(seed=60 + cfg, m=70, n=520, k=1024, device=DEV)
     qa, sa = torch.ops.strix.fp8_quant_group128(d["x"])

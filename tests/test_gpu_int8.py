@@ -54,7 +54,7 @@ def test_accumulator_shapes(m, n, k):
     assert peak_rel_err(out, oracle.w8a8_int8_gemm(q, s, d["w"], d["sw"])) <= TOL
 
 
-@pytest.mark.parametrize("cfg", range(12))
+@pytest.mark.parametrize("cfg", range(13))
 def test_every_cfg_bit_exact(cfg):
     d, q, s = _case(70, 512, 1024, seed=cfg)
     g = torch.ops.strix.w8a8_scaled_mm_cfg(q.to(DEV), s.to(DEV), d["w"].to(DEV), d["sw"].to(DEV), cfg)
