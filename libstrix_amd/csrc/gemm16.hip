@@ -626,22 +626,34 @@ __global__ void __launch_bounds__((WM * WN + NP) * 64) tiled16_kernel(G16 p, int
   auto clampk = [&](int kb) { return kb < nkb ? kb : nkb - 1; };
   auto compute = [&](int kb) {
     const uint8_t* st = smem + (kb % STAGES) * STAGE;
+    auto mma = [&](const u32x4& a, const u32x4& b, v4f& c) {
+      if constexpr (F16) c = mfma_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c);
+      else c = mfma_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c);
+    };
+    u32x4 af0[NT], af1[NT];
+#pragma unroll
+    for (int s = 0; s < NT; ++s) af0[s] = lds128(st + aidx[s] * 2048 + frag0);
 #pragma unroll
     for (int step = 0; step < 2; ++step) {
       const uint32_t fo = step ? frag1 : frag0;
-      u32x4 bf[MT];
+      u32x4 bq[3];
+      bq[0] = lds128(st + (SA + wm * MT) * 2048 + fo);
+      if (MT > 1) bq[1] = lds128(st + (SA + wm * MT + 1) * 2048 + fo);
 #pragma unroll
-      for (int t = 0; t < MT; ++t) bf[t] = lds128(st + (SA + wm * MT + t) * 2048 + fo);
+      for (int t = 0; t < MT; ++t) {
+        if (t + 2 < MT) bq[(t + 2) % 3] = lds128(st + (SA + wm * MT + t + 2) * 2048 + fo);
+        if (step == 0 && t == MT - 2) {
 #pragma unroll
-      for (int s = 0; s < NT; ++s) {
-        const u32x4 af = lds128(st + aidx[s] * 2048 + fo);
-#pragma unroll
-        for (int t = 0; t < MT; ++t) {
-          if constexpr (F16)
-            acc[s][t] = mfma_f16(__builtin_bit_cast(f16x8, af), __builtin_bit_cast(f16x8, bf[t]), acc[s][t]);
-          else
-            acc[s][t] = mfma_bf16(__builtin_bit_cast(bf16x8, af), __builtin_bit_cast(bf16x8, bf[t]), acc[s][t]);
+          for (int s = 0; s < NT; ++s) af1[s] = lds128(st + aidx[s] * 2048 + frag1);
         }
+#pragma unroll
+        for (int s = 0; s < NT; ++s) mma(step ? af1[s] : af0[s], bq[t % 3], acc[s][t]);
+        // One scheduling region per token row: the read two rows ahead goes
+        // out before this row's MFMAs, so each fragment has about seven MFMAs
+        // of cover before its use (the compiler's own order waited on every
+        // pair of reads right after issuing them; C4 T=2048 2-7 % faster,
+        // bit-identical).
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
   };
