@@ -757,6 +757,22 @@ __global__ void __launch_bounds__(WM * WN * 64) tiled8_kernel(G8 p, int tiles_m,
 #pragma unroll
   for (int s0 = 0; s0 < STAGES - 1; ++s0)
     if (s0 < nkb) issue(s0, s0);
+  // The last subtile's partial products of a K block are folded at the start
+  // of the next block (under its first MFMAs) instead of at the end of their
+  // own, and once more after the loop. acc[NT-1] receives the same additions
+  // in the same order, so the result is unchanged; before the first block the
+  // carried values are zeros and their fold adds exactly nothing.
+  v4f prev_f[MT];
+  v4i prev_i[MT];
+  float prev_sw[4] = {0.f, 0.f, 0.f, 0.f};  // weight scale(s) of the previous subtile
+  float prev_sa[MT], prev_c1[MT];             // the carried subtile's activation scales / products
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    prev_f[t] = v4f{0.f, 0.f, 0.f, 0.f};
+    prev_i[t] = v4i{0, 0, 0, 0};
+    prev_sa[t] = 0.f;
+    prev_c1[t] = 0.f;
+  }
 
   for (int kb = 0; kb < nkb; ++kb) {
     const int buf = kb % STAGES;
@@ -801,9 +817,6 @@ __global__ void __launch_bounds__(WM * WN * 64) tiled8_kernel(G8 p, int tiles_m,
     // instructions in that step; the group barriers interleave one MFMA with
     // the fold of one earlier result.
     v8i afc = afrag(0);
-    v4f prev_f[MT];
-    v4i prev_i[MT];
-    float prev_sw[4];  // weight scale(s) of the previous subtile
 #pragma unroll
     for (int s = 0; s < NT; ++s) {
       v8i afn;
@@ -846,6 +859,16 @@ __global__ void __launch_bounds__(WM * WN * 64) tiled8_kernel(G8 p, int tiles_m,
               const float v = (KIND == kFp8Block) ? prev_f[t][i] : (float)prev_i[t][i];
               acc[s - 1][t][i] = fmaf(v, fold_c(prev_sw, t, i), acc[s - 1][t][i]);
             }
+        } else {
+#pragma unroll
+          for (int t = 0; t < MT; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const float v = (KIND == kFp8Block) ? prev_f[t][i] : (float)prev_i[t][i];
+              const float c = (KIND == kFp8Block) ? (ONE_SW ? prev_c1[t] : prev_sw[0] * prev_sa[t])
+                                                  : prev_sw[i] * prev_sa[t];
+              acc[NT - 1][t][i] = fmaf(v, c, acc[NT - 1][t][i]);
+            }
         }
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
@@ -861,7 +884,7 @@ __global__ void __launch_bounds__(WM * WN * 64) tiled8_kernel(G8 p, int tiles_m,
         for (int t = 0; t < MT; ++t) {
           __builtin_amdgcn_sched_group_barrier(0x008, KIND == kFp8Block ? 1 : 2, 0);
           if (t == 0 && s + 1 < NT) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-          if (s > 0) __builtin_amdgcn_sched_group_barrier(0x002, KIND == kFp8Block ? 4 : 8, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, KIND == kFp8Block ? 4 : 8, 0);
         }
       }
       if (s + 1 < NT) afc = afn;
@@ -869,14 +892,21 @@ __global__ void __launch_bounds__(WM * WN * 64) tiled8_kernel(G8 p, int tiles_m,
     }
     if constexpr (!INT_ACC) {
 #pragma unroll
-      for (int t = 0; t < MT; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float v = (KIND == kFp8Block) ? prev_f[t][i] : (float)prev_i[t][i];
-          const float c = (KIND == kFp8Block) ? (ONE_SW ? c1[t] : prev_sw[0] * sa_t[t]) : prev_sw[i] * sa_t[t];
-          acc[NT - 1][t][i] = fmaf(v, c, acc[NT - 1][t][i]);
-        }
+      for (int t = 0; t < MT; ++t) {
+        prev_sa[t] = sa_t[t];
+        if constexpr (KIND == kFp8Block && ONE_SW) prev_c1[t] = c1[t];
+      }
     }
+  }
+  if constexpr (!INT_ACC) {
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float v = (KIND == kFp8Block) ? prev_f[t][i] : (float)prev_i[t][i];
+        const float c = (KIND == kFp8Block) ? (ONE_SW ? prev_c1[t] : prev_sw[0] * prev_sa[t]) : prev_sw[i] * prev_sa[t];
+        acc[NT - 1][t][i] = fmaf(v, c, acc[NT - 1][t][i]);
+      }
   }
 
   // Epilogue straight from registers.
