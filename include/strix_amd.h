@@ -216,6 +216,18 @@ int strix_moe_route_align(const void* logits, int logits_dtype, int64_t ldl, int
                           int renormalize, int32_t* topk_ids, float* topk_weights, int64_t block_m,
                           int32_t* sorted_ids, int64_t sorted_cap, int32_t* expert_ids, int64_t blocks_cap,
                           int32_t* num_post, void* workspace, int64_t workspace_bytes, void* stream);
+/* strix_moe_route_align plus the tokens' e4m3 1x128 quantization
+ * (strix_fp8_quant_group128 of x [T, K] into q, s), the steps the reference's
+ * FP8 MoE forward runs first (python/strix_vllm/moe.py:181-184, 905-1014).
+ * Up to 16 tokens the single-block kernel quantizes the rows with the waves
+ * the router leaves idle, so the three steps are one launch; above, the
+ * separate kernels run in turn. Same outputs, bit for bit. */
+int strix_moe_route_align_quant(const void* logits, int logits_dtype, int64_t ldl, int64_t T, int64_t E,
+                                int64_t top_k, int renormalize, int32_t* topk_ids, float* topk_weights,
+                                int64_t block_m, int32_t* sorted_ids, int64_t sorted_cap, int32_t* expert_ids,
+                                int64_t blocks_cap, int32_t* num_post, void* workspace, int64_t workspace_bytes,
+                                const void* x, int x_dtype, int64_t ldx, uint8_t* q, int64_t ldq, float* s,
+                                int64_t lds, int64_t K, void* stream);
 /* moe_sum (python/strix_vllm/moe.py:328-330): out[t] = sum_j w[t,j] * y[t*k+j]
  * (w NULL = unweighted), fp32 in slot order. */
 int strix_moe_sum(const void* y, int dtype, int64_t ldy, int64_t T, int64_t top_k, int64_t H,

@@ -12,6 +12,7 @@
 //           slots appear in ascending order, each expert's run is padded to a
 //           multiple of block_m with the id S = T*top_k.
 #include "capi_internal.h"
+#include "quant_common.h"
 #include "strix_common.h"
 
 namespace strix {
@@ -260,18 +261,47 @@ __global__ void __launch_bounds__(1024)
   align_block(ids, S, E, block_m, sorted_ids, sorted_cap, expert_ids, blocks_cap, num_post, cnt, off, wave_tot);
 }
 
+// The tokens' e4m3 1x128 quantization that the fused router may do on the
+// side (x == nullptr: none): x [T, K] bf16/fp16 -> q [T, K] e4m3, s [T, K/128].
+struct ActQuant {
+  const uint16_t* x;
+  int64_t ldx;
+  uint8_t* q;
+  int64_t ldq;
+  float* s;
+  int64_t lds;
+  int K;
+  int f16;
+};
+
+// Threads [0, nthreads) of the block (whole waves) quantize rows [0, M).
+__device__ __forceinline__ void quant_rows(const ActQuant& a, int M, int tid, int nthreads) {
+  const uint32_t gpr = (uint32_t)(a.K >> 7), total = (uint32_t)M * gpr;
+  const uint32_t per_pass = (uint32_t)nthreads >> 3;
+  for (uint32_t base = 0; base < total; base += per_pass) {  // the same trip count in every lane
+    const uint32_t grp = base + ((uint32_t)tid >> 3);
+    const bool live = grp < total;
+    const uint32_t m = live ? grp / gpr : 0u, g = live ? grp - m * gpr : 0u;
+    if (a.f16) quant128_lane<true, true>(a.x, a.ldx, a.q, a.ldq, a.s, a.lds, m, g, tid & 7, live);
+    else quant128_lane<false, true>(a.x, a.ldx, a.q, a.ldq, a.s, a.lds, m, g, tid & 7, live);
+  }
+}
+
 // Router and align in one block: 16 waves route the T tokens (T * k <= 1024),
-// then the block aligns the slot ids it just produced.
+// then the block aligns the slot ids it just produced. With `act`, the block
+// also quantizes the T token rows: waves past the last token do it while the
+// router runs (all 16 waves after the align when T is 16).
 template <bool BF16_LOGITS, int PER>
 __global__ void __launch_bounds__(1024)
     route_align_small_kernel(const void* __restrict__ logits, int64_t ldl, int T, int E, int k, int renorm,
                              int32_t* __restrict__ topk_ids, float* __restrict__ topk_w, int block_m,
                              int32_t* __restrict__ sorted_ids, int64_t sorted_cap, int32_t* __restrict__ expert_ids,
-                             int64_t blocks_cap, int32_t* __restrict__ num_post) {
+                             int64_t blocks_cap, int32_t* __restrict__ num_post, ActQuant act) {
   __shared__ __align__(16) int32_t ids[kAlignSmall];
   __shared__ int cnt[1024], off[1024], wave_tot[16];
   __shared__ RouteScratch scratch[16];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (act.x != nullptr && T < 16 && wave >= T) quant_rows(act, T, threadIdx.x - 64 * T, 64 * (16 - T));
   for (int t = wave; t < T; t += 16) {
     int my_id = 0;
     const float w = route_token<BF16_LOGITS, PER>(logits, ldl, t, E, k, renorm, my_id, scratch[wave]);
@@ -283,6 +313,7 @@ __global__ void __launch_bounds__(1024)
   }
   __syncthreads();
   align_block(ids, T * k, E, block_m, sorted_ids, sorted_cap, expert_ids, blocks_cap, num_post, cnt, off, wave_tot);
+  if (act.x != nullptr && T >= 16) quant_rows(act, T, threadIdx.x, 1024);
 }
 
 // ---- align, pass 1: per-chunk histograms. Chunk c covers slots [256c, 256c+256).
@@ -541,19 +572,26 @@ int strix_moe_align(const int32_t* topk_ids, int64_t num_slots, int64_t E, int64
   return check_launch(op);
 }
 
-int strix_moe_route_align(const void* logits, int logits_dtype, int64_t ldl, int64_t T, int64_t E, int64_t top_k,
-                          int renormalize, int32_t* topk_ids, float* topk_weights, int64_t block_m,
-                          int32_t* sorted_ids, int64_t sorted_cap, int32_t* expert_ids, int64_t blocks_cap,
-                          int32_t* num_post, void* workspace, int64_t workspace_bytes, void* stream) {
-  const char* op = "moe_route_align";
+}  // extern "C"
+
+namespace strix {
+namespace {
+
+int route_align_impl(const char* op, const void* logits, int logits_dtype, int64_t ldl, int64_t T, int64_t E,
+                     int64_t top_k, int renormalize, int32_t* topk_ids, float* topk_weights, int64_t block_m,
+                     int32_t* sorted_ids, int64_t sorted_cap, int32_t* expert_ids, int64_t blocks_cap,
+                     int32_t* num_post, void* workspace, int64_t workspace_bytes, const ActQuant& act,
+                     int x_dtype, void* stream) {
   // One block routes at most one token per wave (16 tokens) before the
   // separate, grid-wide router is faster.
   if (T * top_k > kAlignSmall || T > 16 || T == 0) {
     int rc = strix_moe_route_topk(logits, logits_dtype, ldl, T, E, top_k, renormalize, topk_ids, topk_weights, top_k,
                                   stream);
     if (rc) return rc;
-    return strix_moe_align(topk_ids, T * top_k, E, block_m, sorted_ids, sorted_cap, expert_ids, blocks_cap, num_post,
-                           workspace, workspace_bytes, stream);
+    rc = strix_moe_align(topk_ids, T * top_k, E, block_m, sorted_ids, sorted_cap, expert_ids, blocks_cap, num_post,
+                         workspace, workspace_bytes, stream);
+    if (rc || act.x == nullptr) return rc;
+    return strix_fp8_quant_group128(act.x, x_dtype, act.ldx, act.q, act.ldq, act.s, act.lds, T, act.K, stream);
   }
   STRIX_REQUIRE(logits_dtype == STRIX_F32 || logits_dtype == STRIX_BF16, "%s: logits must be float32 or bfloat16", op);
   STRIX_REQUIRE(E >= 1 && E <= 64 * kMaxExpertsPerLane, "%s: 1 <= E <= %d, got E=%lld", op,
@@ -570,10 +608,54 @@ int strix_moe_route_align(const void* logits, int logits_dtype, int64_t ldl, int
     constexpr int PER = decltype(per_tag)::value;
     hipLaunchKernelGGL((route_align_small_kernel<BF, PER>), dim3(1), dim3(1024), 0, as_stream(stream), logits, ldl,
                        (int)T, (int)E, (int)top_k, renormalize, topk_ids, topk_weights, (int)block_m, sorted_ids,
-                       sorted_cap, expert_ids, blocks_cap, num_post);
+                       sorted_cap, expert_ids, blocks_cap, num_post, act);
   };
   per_dispatch(E, logits_dtype == STRIX_BF16, go);
   return check_launch(op);
+}
+
+}  // namespace
+}  // namespace strix
+
+extern "C" {
+
+int strix_moe_route_align(const void* logits, int logits_dtype, int64_t ldl, int64_t T, int64_t E, int64_t top_k,
+                          int renormalize, int32_t* topk_ids, float* topk_weights, int64_t block_m,
+                          int32_t* sorted_ids, int64_t sorted_cap, int32_t* expert_ids, int64_t blocks_cap,
+                          int32_t* num_post, void* workspace, int64_t workspace_bytes, void* stream) {
+  const ActQuant none = {};
+  return route_align_impl("moe_route_align", logits, logits_dtype, ldl, T, E, top_k, renormalize, topk_ids,
+                          topk_weights, block_m, sorted_ids, sorted_cap, expert_ids, blocks_cap, num_post, workspace,
+                          workspace_bytes, none, STRIX_BF16, stream);
+}
+
+int strix_moe_route_align_quant(const void* logits, int logits_dtype, int64_t ldl, int64_t T, int64_t E,
+                                int64_t top_k, int renormalize, int32_t* topk_ids, float* topk_weights,
+                                int64_t block_m, int32_t* sorted_ids, int64_t sorted_cap, int32_t* expert_ids,
+                                int64_t blocks_cap, int32_t* num_post, void* workspace, int64_t workspace_bytes,
+                                const void* x, int x_dtype, int64_t ldx, uint8_t* q, int64_t ldq, float* s,
+                                int64_t lds, int64_t K, void* stream) {
+  const char* op = "moe_route_align_quant";
+  STRIX_REQUIRE(x != nullptr && q != nullptr && s != nullptr, "%s: x, q and s are required", op);
+  STRIX_REQUIRE(x_dtype == STRIX_BF16 || x_dtype == STRIX_F16, "%s: activation must be float16 or bfloat16", op);
+  STRIX_REQUIRE(K > 0 && K % 128 == 0 && K <= INT32_MAX, "%s: K must be a positive multiple of 128, got K=%lld", op,
+                (long long)K);
+  STRIX_REQUIRE(ldx >= K && ldx % 8 == 0 && ldq >= K && ldq % 8 == 0 && lds >= K / 128,
+                "%s: activation, output and scale row strides must cover K (multiples of 8)", op);
+  STRIX_REQUIRE(aligned(x, 16) && aligned(q, 8), "%s: activation must be 16-byte aligned and output 8-byte aligned",
+                op);
+  ActQuant act;
+  act.x = static_cast<const uint16_t*>(x);
+  act.ldx = ldx;
+  act.q = q;
+  act.ldq = ldq;
+  act.s = s;
+  act.lds = lds;
+  act.K = (int)K;
+  act.f16 = x_dtype == STRIX_F16;
+  return route_align_impl(op, logits, logits_dtype, ldl, T, E, top_k, renormalize, topk_ids, topk_weights, block_m,
+                          sorted_ids, sorted_cap, expert_ids, blocks_cap, num_post, workspace, workspace_bytes, act,
+                          x_dtype, stream);
 }
 
 int strix_moe_sum(const void* y, int dtype, int64_t ldy, int64_t T, int64_t top_k, int64_t H,

@@ -11,45 +11,16 @@
 //
 // The division is IEEE (correctly rounded), so the CPU oracle reproduces q
 // bit for bit; the e4m3 quantizer gets the same bytes from a reciprocal
-// product, with the division kept where the product could round differently. In the 128-group quantizers each lane owns 16 consecutive
+// product, with the division kept where the product could round
+// differently. In the 128-group quantizers each lane owns 16 consecutive
 // elements (two 16-byte loads); a group is 8 lanes, so the group max is an
-// 8-lane butterfly.
+// 8-lane butterfly (quant_common.h).
 #include "capi_internal.h"
+#include "quant_common.h"
 #include "strix_common.h"
 
 namespace strix {
 namespace {
-
-template <bool F16>
-__device__ __forceinline__ void load8(const uint16_t* p, float v[8]) {
-  const u32x4 raw = *reinterpret_cast<const u32x4*>(p);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    v[2 * i] = act_to_f32<F16>(raw[i] & 0xffffu);
-    v[2 * i + 1] = act_to_f32<F16>(raw[i] >> 16);
-  }
-}
-
-// x / sc correctly rounded, as far as the e4m3 rounding that follows can
-// tell. x * RN(1/sc) is within 1.5 ulp of x / sc, so both round to the same
-// e4m3 value unless the product lies in e4m3's subnormal range or within 4
-// ulp of an e4m3 rounding midpoint (low 20 mantissa bits near 0x80000); those
-// elements, and groups whose scale is subnormal (1/sc would overflow), take
-// the IEEE division. tests/test_e4m3_quotient.py checks the argument on the
-// CPU for every 16-bit x against sampled group maxima.
-__device__ __forceinline__ float div_for_e4m3(float x, float sc, float r, bool fast) {
-  float q = x * r;
-  const uint32_t b = __float_as_uint(q) & 0x7fffffffu;
-  const int d = (int)(b & 0xfffffu) - 0x80000;
-  if (!fast || b - 1u < (121u << 23) - 1u || (unsigned)(d + 4) <= 8u) q = __fdiv_rn(x, sc);
-  return q;
-}
-
-__device__ __forceinline__ int q_i8(float x, float s) {
-  float r = __builtin_rintf(__fdiv_rn(x, s));
-  r = fminf(fmaxf(r, -127.0f), 127.0f);
-  return (int)r;
-}
 
 // One 256-thread block per row.
 template <bool F16>
@@ -101,44 +72,7 @@ __global__ void __launch_bounds__(256)
   const bool live = grp < total_groups;
   const uint32_t m = live ? grp / groups_per_row : 0u;
   const uint32_t g = live ? grp - m * groups_per_row : 0u;
-  const int64_t k = (int64_t)g * 128 + sub * 16;
-  float v[16];
-  if (live) {
-    const uint16_t* p = x + (int64_t)m * ldx + k;
-    load8<F16>(p, v);
-    load8<F16>(p + 8, v + 8);
-  } else {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) v[i] = 0.0f;
-  }
-  float mx = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) mx = fmaxf(mx, fabsf(v[i]));
-#pragma unroll
-  for (int o = 4; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
-  const float qmax = FP8 ? 448.0f : 127.0f;
-  const float sc = mx > 0.0f ? __fdiv_rn(mx, qmax) : 1.0f;
-  if (!live) return;
-  if (sub == 0) s[(int64_t)m * lds + g] = sc;
-  const bool fast = sc >= 0x1p-126f;
-  const float rs = FP8 ? __fdiv_rn(1.0f, sc) : 0.0f;
-  uint32_t w[4] = {0u, 0u, 0u, 0u};
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const float* u = v + 4 * j;
-    if constexpr (FP8) {
-      int r = 0;
-      r = cvt_pk_e4m3<false>(div_for_e4m3(u[0], sc, rs, fast), div_for_e4m3(u[1], sc, rs, fast), r);
-      r = cvt_pk_e4m3<true>(div_for_e4m3(u[2], sc, rs, fast), div_for_e4m3(u[3], sc, rs, fast), r);
-      w[j] = (uint32_t)r;
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) w[j] |= (uint32_t)(q_i8(u[i], sc) & 0xff) << (8 * i);
-    }
-  }
-  uint2* out = reinterpret_cast<uint2*>(q + (int64_t)m * ldq + k);  // output rows are 8-byte aligned
-  out[0] = make_uint2(w[0], w[1]);
-  out[1] = make_uint2(w[2], w[3]);
+  quant128_lane<F16, FP8>(x, ldx, q, ldq, s, lds, m, g, sub, live);
 }
 
 template <bool F16>

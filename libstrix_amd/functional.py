@@ -62,8 +62,7 @@ def fused_moe_fp8_w8a8(x, logits, w13, w13_s, w2, w2_s, top_k: int, renormalize:
     e, n13 = w13.size(0), (w13.size(2) if w13.dim() == 4 else w13.size(1))
     inter = n13 // 2
     bm = block_m or moe_block_m(t, top_k, e)
-    ids, w, sorted_ids, expert_ids, num_post = route_and_align(logits, top_k, e, bm, renormalize)
-    qx, sx = S.fp8_quant_group128(x)
+    ids, w, sorted_ids, expert_ids, num_post, qx, sx = S.moe_route_align_quant(logits, x, top_k, bm, renormalize)
     slots = t * top_k
     h13 = torch.empty((slots, inter), dtype=torch.bfloat16, device=x.device)
     S.moe_gemm_fp8_w8a8(h13, qx, sx, w13, w13_s, sorted_ids, expert_ids, num_post, None, top_k, bm, 128, True,

@@ -216,6 +216,21 @@ KERNELS: list[Kernel] = [
          "num_slots": Range(hi=1024)},
     ),
     Kernel(
+        "moe_route_align_quant",
+        "moe_route_align_quant_small",
+        "moe_route_align_small plus the tokens' e4m3 1x128 quantization, done by the waves the router leaves "
+        "idle: router, align and quantizer in one launch",
+        {"logits_dtype": ("fp32", "bf16"), "dtype": ("bf16", "fp16"), "num_experts": Range(hi=1024),
+         "tokens": Range(lo=1, hi=16), "num_slots": Range(hi=1024), "group_size": 128},
+    ),
+    Kernel(
+        "moe_route_align_quant",
+        "moe_route_align_then_quant",
+        "moe_route_align then fp8_quant_group128 (above 16 tokens or 1024 slots)",
+        {"logits_dtype": ("fp32", "bf16"), "dtype": ("bf16", "fp16"), "num_experts": Range(hi=1024),
+         "group_size": 128},
+    ),
+    Kernel(
         "moe_route_align",
         "moe_route_then_align",
         "moe_route_topk (one wave per token, grid-wide) then moe_align",

@@ -459,6 +459,49 @@ def _(logits, top_k, block_m, renormalize=True):
             logits.new_empty((cap,), dtype=i32), logits.new_empty((nblk,), dtype=i32), logits.new_empty((1,), dtype=i32))
 
 
+@_define(
+    "moe_route_align_quant(Tensor logits, Tensor x, int top_k, int block_m, bool renormalize=True) -> "
+    "(Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)"
+)
+def moe_route_align_quant(logits, x, top_k, block_m, renormalize=True):
+    """moe_route_align and fp8_quant_group128(x) in one call: (topk_ids,
+    topk_weights, sorted_ids, expert_ids, num_post_padded, qx, sx), the same
+    bits as the two ops; up to 16 tokens it is one kernel launch."""
+    _rowmajor(logits, "logits")
+    _rowmajor(x, "x")
+    _check(logits.dtype in (torch.float32, torch.bfloat16), "logits must be float32 or bfloat16")
+    t, e = logits.shape
+    _check(x.size(0) == t, "x must have one row per token")
+    k = x.size(1)
+    dev = logits.device
+    ids = torch.empty((t, top_k), dtype=torch.int32, device=dev)
+    w = torch.empty((t, top_k), dtype=torch.float32, device=dev)
+    cap, nblk = align_capacity(t * top_k, e, block_m)
+    sorted_ids = torch.empty((cap,), dtype=torch.int32, device=dev)
+    expert_ids = torch.empty((nblk,), dtype=torch.int32, device=dev)
+    num_post = torch.empty((1,), dtype=torch.int32, device=dev)
+    q = torch.empty((t, k), dtype=torch.float8_e4m3fn, device=dev)
+    s = torch.empty((t, k // 128), dtype=torch.float32, device=dev)
+    ws_bytes = _lib.query("strix_moe_align_workspace_bytes", t * top_k, e)
+    ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev)
+    code = _lib.F32 if logits.dtype == torch.float32 else _lib.BF16
+    _lib.call("strix_moe_route_align_quant", _ptr(logits), code, logits.stride(0), t, e, top_k,
+              int(bool(renormalize)), _ptr(ids), _ptr(w), block_m, _ptr(sorted_ids), cap, _ptr(expert_ids), nblk,
+              _ptr(num_post), _ptr(ws), ws_bytes, _ptr(x), _act_code(x), x.stride(0), _ptr(q), k, _ptr(s),
+              max(k // 128, 1), k, _stream(logits))
+    return ids, w, sorted_ids, expert_ids, num_post, q, s
+
+
+@_fake("moe_route_align_quant")
+def _(logits, x, top_k, block_m, renormalize=True):
+    t, e = logits.shape
+    cap, nblk = align_capacity(t * top_k, e, block_m)
+    i32 = torch.int32
+    return (logits.new_empty((t, top_k), dtype=i32), logits.new_empty((t, top_k), dtype=torch.float32),
+            logits.new_empty((cap,), dtype=i32), logits.new_empty((nblk,), dtype=i32), logits.new_empty((1,), dtype=i32),
+            x.new_empty(x.shape, dtype=torch.float8_e4m3fn), x.new_empty((t, x.size(1) // 128), dtype=torch.float32))
+
+
 def _sum_impl(inp, weights, output):
     _check(inp.dim() == 3 and inp.is_contiguous(), "input must be contiguous [T, top_k, H]")
     t, k, h = inp.shape

@@ -209,3 +209,22 @@ def test_fused_moe_kmajor_weights_bit_identical(t):
     assert w13k.shape == (128, 16, 1536, 128) and w2k.shape == (128, 6, 2048, 128)
     got = functional.fused_moe_fp8_w8a8(x, logits, w13k, c3["w13_s"], w2k, c3["w2_s"], 8)
     assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("t", [1, 3, 15, 16, 17, 64, 300])
+@pytest.mark.parametrize("xdtype", [torch.bfloat16, torch.float16])
+def test_route_align_quant_matches_separate_ops(t, xdtype):
+    # Up to 16 tokens one kernel routes, aligns and quantizes (idle waves
+    # quantize while the router runs; all waves after the align at 16); above,
+    # the separate kernels run. Either way: the same bits as the two ops.
+    g = torch.Generator().manual_seed(100 + t)
+    logits = torch.randn(t, 128, generator=g).to(DEV)
+    x = (torch.randn(t, 2048, generator=g) * 3).to(xdtype).to(DEV)
+    if t > 2:
+        x[1, 256:384] = 0  # an all-zero group takes scale 1
+    got = torch.ops.strix.moe_route_align_quant(logits, x, 8, 16)
+    want = torch.ops.strix.moe_route_align(logits, 8, 16) + torch.ops.strix.fp8_quant_group128(x)
+    for a, b in zip(got, want):
+        if a.dtype == torch.float8_e4m3fn:
+            a, b = a.view(torch.uint8), b.view(torch.uint8)
+        assert torch.equal(a, b)
