@@ -206,6 +206,17 @@ int64_t strix_moe_align_workspace_bytes(int64_t num_slots, int64_t E);
 int strix_moe_align(const int32_t* topk_ids, int64_t num_slots, int64_t E, int64_t block_m,
                     int32_t* sorted_ids, int64_t sorted_cap, int32_t* expert_ids, int64_t blocks_cap,
                     int32_t* num_post, void* workspace, int64_t workspace_bytes, void* stream);
+/* strix_moe_align plus the tokens' e4m3 1x128 quantization
+ * (strix_fp8_quant_group128 of x [T, K] into q, s): the align and the
+ * activation quant the reference's FP8 expert forward runs after vLLM's
+ * router (python/strix_vllm/moe.py:286-288, 905-1014). Up to 1024 slots and
+ * 64 tokens both run in the single-block align launch; otherwise in turn.
+ * Same outputs, bit for bit. */
+int strix_moe_align_quant(const int32_t* topk_ids, int64_t num_slots, int64_t E, int64_t block_m,
+                          int32_t* sorted_ids, int64_t sorted_cap, int32_t* expert_ids, int64_t blocks_cap,
+                          int32_t* num_post, void* workspace, int64_t workspace_bytes, const void* x, int x_dtype,
+                          int64_t ldx, uint8_t* q, int64_t ldq, float* s, int64_t lds, int64_t T, int64_t K,
+                          void* stream);
 /* Router and align in one call: the reference runs vLLM's fused_topk then
  * moe_align_block_size (python/strix_vllm/moe.py:181-184, 286-288). Same
  * outputs as strix_moe_route_topk (ldo = top_k) followed by strix_moe_align;

@@ -60,6 +60,7 @@ SIGNATURES: dict[str, list] = {
     "strix_moe_align_sorted_capacity": [L, L, L],
     "strix_moe_align_workspace_bytes": [L, L],
     "strix_moe_align": [P, L, L, L, P, L, P, L, P, P, L, P],
+    "strix_moe_align_quant": [P, L, L, L, P, L, P, L, P, P, L, P, I, L, P, L, P, L, L, L, P],
     "strix_moe_route_align": [P, I, L, L, L, L, I, P, P, L, P, L, P, L, P, P, L, P],
     "strix_moe_route_align_quant": [P, I, L, L, L, L, I, P, P, L, P, L, P, L, P, P, L, P, I, L, P, L, P, L, L, P],
     "strix_moe_sum": [P, I, L, L, L, L, P, P, L, P],

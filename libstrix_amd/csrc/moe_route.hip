@@ -250,19 +250,8 @@ __device__ void align_block(const int32_t* ids, int S, int E, int block_m, int32
   }
 }
 
-__global__ void __launch_bounds__(1024)
-    align_small_kernel(const int32_t* __restrict__ topk_ids, int S, int E, int block_m,
-                       int32_t* __restrict__ sorted_ids, int64_t sorted_cap, int32_t* __restrict__ expert_ids,
-                       int64_t blocks_cap, int32_t* __restrict__ num_post) {
-  __shared__ __align__(16) int32_t ids[kAlignSmall];
-  __shared__ int cnt[1024], off[1024], wave_tot[16];
-  if ((int)threadIdx.x < S) ids[threadIdx.x] = topk_ids[threadIdx.x];
-  __syncthreads();
-  align_block(ids, S, E, block_m, sorted_ids, sorted_cap, expert_ids, blocks_cap, num_post, cnt, off, wave_tot);
-}
-
-// The tokens' e4m3 1x128 quantization that the fused router may do on the
-// side (x == nullptr: none): x [T, K] bf16/fp16 -> q [T, K] e4m3, s [T, K/128].
+// The tokens' e4m3 1x128 quantization that the single-block align and router
+// kernels may do on the side (x == nullptr: none): x [T, K] bf16/fp16 -> q [T, K] e4m3, s [T, K/128].
 struct ActQuant {
   const uint16_t* x;
   int64_t ldx;
@@ -286,6 +275,21 @@ __device__ __forceinline__ void quant_rows(const ActQuant& a, int M, int tid, in
     else quant128_lane<false, true>(a.x, a.ldx, a.q, a.ldq, a.s, a.lds, m, g, tid & 7, live);
   }
 }
+
+// With `act`, the block quantizes the T token rows after the align (T <= 64,
+// checked on the host).
+__global__ void __launch_bounds__(1024)
+    align_small_kernel(const int32_t* __restrict__ topk_ids, int S, int E, int block_m,
+                       int32_t* __restrict__ sorted_ids, int64_t sorted_cap, int32_t* __restrict__ expert_ids,
+                       int64_t blocks_cap, int32_t* __restrict__ num_post, ActQuant act, int T) {
+  __shared__ __align__(16) int32_t ids[kAlignSmall];
+  __shared__ int cnt[1024], off[1024], wave_tot[16];
+  if ((int)threadIdx.x < S) ids[threadIdx.x] = topk_ids[threadIdx.x];
+  __syncthreads();
+  align_block(ids, S, E, block_m, sorted_ids, sorted_cap, expert_ids, blocks_cap, num_post, cnt, off, wave_tot);
+  if (act.x != nullptr) quant_rows(act, T, threadIdx.x, 1024);
+}
+
 
 // Router and align in one block: 16 waves route the T tokens (T * k <= 1024),
 // then the block aligns the slot ids it just produced. With `act`, the block
@@ -537,10 +541,14 @@ int64_t strix_moe_align_workspace_bytes(int64_t num_slots, int64_t E) {
   return (chunks > 0 ? chunks : 1) * E * 4;
 }
 
-int strix_moe_align(const int32_t* topk_ids, int64_t num_slots, int64_t E, int64_t block_m,
-                    int32_t* sorted_ids, int64_t sorted_cap, int32_t* expert_ids, int64_t blocks_cap,
-                    int32_t* num_post, void* workspace, int64_t workspace_bytes, void* stream) {
-  const char* op = "moe_align";
+}  // extern "C"
+
+namespace strix {
+namespace {
+
+int align_impl(const char* op, const int32_t* topk_ids, int64_t num_slots, int64_t E, int64_t block_m,
+               int32_t* sorted_ids, int64_t sorted_cap, int32_t* expert_ids, int64_t blocks_cap, int32_t* num_post,
+               void* workspace, int64_t workspace_bytes, const ActQuant& act, int64_t T, int x_dtype, void* stream) {
   STRIX_REQUIRE(E >= 1 && E <= 1024, "%s: 1 <= E <= 1024, got %lld", op, (long long)E);
   STRIX_REQUIRE(block_m >= 1 && block_m <= 1024, "%s: block_m must be in 1..1024", op);
   STRIX_REQUIRE(num_slots >= 0 && num_slots < INT32_MAX / 2, "%s: bad slot count", op);
@@ -552,10 +560,16 @@ int strix_moe_align(const int32_t* topk_ids, int64_t num_slots, int64_t E, int64
   STRIX_ARCH_GATE();
   hipStream_t st = as_stream(stream);
   const int S = (int)num_slots;
+  // One block also quantizes up to 64 token rows (at most 8 passes of its
+  // threads); more rows, or more slots, take the separate quantizer.
+  const bool fuse = act.x != nullptr && T <= 64;
   if (S <= kAlignSmall) {
+    const ActQuant none = {};
     hipLaunchKernelGGL(align_small_kernel, dim3(1), dim3(1024), 0, st, topk_ids, S, (int)E, (int)block_m, sorted_ids,
-                       sorted_cap, expert_ids, blocks_cap, num_post);
-    return check_launch(op);
+                       sorted_cap, expert_ids, blocks_cap, num_post, fuse ? act : none, (int)T);
+    int rc = check_launch(op);
+    if (rc || fuse || act.x == nullptr) return rc;
+    return strix_fp8_quant_group128(act.x, x_dtype, act.ldx, act.q, act.ldq, act.s, act.lds, T, act.K, stream);
   }
   const int chunks = (S + 255) / 256;
   int32_t* hist = static_cast<int32_t*>(workspace);
@@ -569,7 +583,59 @@ int strix_moe_align(const int32_t* topk_ids, int64_t num_slots, int64_t E, int64
   rc = check_launch(op);
   if (rc) return rc;
   hipLaunchKernelGGL(align_scatter_kernel, dim3(chunks), dim3(256), 0, st, topk_ids, S, (int)E, hist, sorted_ids);
-  return check_launch(op);
+  rc = check_launch(op);
+  if (rc || act.x == nullptr) return rc;
+  return strix_fp8_quant_group128(act.x, x_dtype, act.ldx, act.q, act.ldq, act.s, act.lds, T, act.K, stream);
+}
+
+// Checks the activation-quantizer arguments of the *_quant entry points and
+// packs them.
+int make_act_quant(const char* op, const void* x, int x_dtype, int64_t ldx, uint8_t* q, int64_t ldq, float* s,
+                   int64_t lds, int64_t K, ActQuant& act) {
+  STRIX_REQUIRE(x != nullptr && q != nullptr && s != nullptr, "%s: x, q and s are required", op);
+  STRIX_REQUIRE(x_dtype == STRIX_BF16 || x_dtype == STRIX_F16, "%s: activation must be float16 or bfloat16", op);
+  STRIX_REQUIRE(K > 0 && K % 128 == 0 && K <= INT32_MAX, "%s: K must be a positive multiple of 128, got K=%lld", op,
+                (long long)K);
+  STRIX_REQUIRE(ldx >= K && ldx % 8 == 0 && ldq >= K && ldq % 8 == 0 && lds >= K / 128,
+                "%s: activation, output and scale row strides must cover K (multiples of 8)", op);
+  STRIX_REQUIRE(aligned(x, 16) && aligned(q, 8), "%s: activation must be 16-byte aligned and output 8-byte aligned",
+                op);
+  act.x = static_cast<const uint16_t*>(x);
+  act.ldx = ldx;
+  act.q = q;
+  act.ldq = ldq;
+  act.s = s;
+  act.lds = lds;
+  act.K = (int)K;
+  act.f16 = x_dtype == STRIX_F16;
+  return STRIX_OK;
+}
+
+}  // namespace
+}  // namespace strix
+
+extern "C" {
+
+int strix_moe_align(const int32_t* topk_ids, int64_t num_slots, int64_t E, int64_t block_m,
+                    int32_t* sorted_ids, int64_t sorted_cap, int32_t* expert_ids, int64_t blocks_cap,
+                    int32_t* num_post, void* workspace, int64_t workspace_bytes, void* stream) {
+  const ActQuant none = {};
+  return align_impl("moe_align", topk_ids, num_slots, E, block_m, sorted_ids, sorted_cap, expert_ids, blocks_cap,
+                    num_post, workspace, workspace_bytes, none, 0, STRIX_BF16, stream);
+}
+
+int strix_moe_align_quant(const int32_t* topk_ids, int64_t num_slots, int64_t E, int64_t block_m,
+                          int32_t* sorted_ids, int64_t sorted_cap, int32_t* expert_ids, int64_t blocks_cap,
+                          int32_t* num_post, void* workspace, int64_t workspace_bytes, const void* x, int x_dtype,
+                          int64_t ldx, uint8_t* q, int64_t ldq, float* s, int64_t lds, int64_t T, int64_t K,
+                          void* stream) {
+  const char* op = "moe_align_quant";
+  ActQuant act;
+  int rc = make_act_quant(op, x, x_dtype, ldx, q, ldq, s, lds, K, act);
+  if (rc) return rc;
+  STRIX_REQUIRE(T >= 0 && T <= num_slots, "%s: bad token count", op);
+  return align_impl(op, topk_ids, num_slots, E, block_m, sorted_ids, sorted_cap, expert_ids, blocks_cap, num_post,
+                    workspace, workspace_bytes, act, T, x_dtype, stream);
 }
 
 }  // extern "C"
@@ -636,23 +702,9 @@ int strix_moe_route_align_quant(const void* logits, int logits_dtype, int64_t ld
                                 const void* x, int x_dtype, int64_t ldx, uint8_t* q, int64_t ldq, float* s,
                                 int64_t lds, int64_t K, void* stream) {
   const char* op = "moe_route_align_quant";
-  STRIX_REQUIRE(x != nullptr && q != nullptr && s != nullptr, "%s: x, q and s are required", op);
-  STRIX_REQUIRE(x_dtype == STRIX_BF16 || x_dtype == STRIX_F16, "%s: activation must be float16 or bfloat16", op);
-  STRIX_REQUIRE(K > 0 && K % 128 == 0 && K <= INT32_MAX, "%s: K must be a positive multiple of 128, got K=%lld", op,
-                (long long)K);
-  STRIX_REQUIRE(ldx >= K && ldx % 8 == 0 && ldq >= K && ldq % 8 == 0 && lds >= K / 128,
-                "%s: activation, output and scale row strides must cover K (multiples of 8)", op);
-  STRIX_REQUIRE(aligned(x, 16) && aligned(q, 8), "%s: activation must be 16-byte aligned and output 8-byte aligned",
-                op);
   ActQuant act;
-  act.x = static_cast<const uint16_t*>(x);
-  act.ldx = ldx;
-  act.q = q;
-  act.ldq = ldq;
-  act.s = s;
-  act.lds = lds;
-  act.K = (int)K;
-  act.f16 = x_dtype == STRIX_F16;
+  int rc = make_act_quant(op, x, x_dtype, ldx, q, ldq, s, lds, K, act);
+  if (rc) return rc;
   return route_align_impl(op, logits, logits_dtype, ldl, T, E, top_k, renormalize, topk_ids, topk_weights, block_m,
                           sorted_ids, sorted_cap, expert_ids, blocks_cap, num_post, workspace, workspace_bytes, act,
                           x_dtype, stream);

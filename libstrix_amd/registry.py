@@ -216,6 +216,19 @@ KERNELS: list[Kernel] = [
          "num_slots": Range(hi=1024)},
     ),
     Kernel(
+        "moe_align_quant",
+        "moe_align_quant_small",
+        "moe_align_small plus the tokens' e4m3 1x128 quantization in the same single-block launch",
+        {"dtype": ("bf16", "fp16"), "num_experts": Range(hi=1024), "num_slots": Range(hi=1024),
+         "tokens": Range(hi=64), "group_size": 128},
+    ),
+    Kernel(
+        "moe_align_quant",
+        "moe_align_then_quant",
+        "moe_align then fp8_quant_group128 (above 1024 slots or 64 tokens)",
+        {"dtype": ("bf16", "fp16"), "num_experts": Range(hi=1024), "group_size": 128},
+    ),
+    Kernel(
         "moe_route_align_quant",
         "moe_route_align_quant_small",
         "moe_route_align_small plus the tokens' e4m3 1x128 quantization, done by the waves the router leaves "

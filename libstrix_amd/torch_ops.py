@@ -425,6 +425,40 @@ def _(topk_ids, num_experts, block_m):
     return (topk_ids.new_empty((cap,)), topk_ids.new_empty((nblk,)), topk_ids.new_empty((1,)))
 
 
+@_define("moe_align_quant(Tensor topk_ids, Tensor x, int num_experts, int block_m) "
+         "-> (Tensor, Tensor, Tensor, Tensor, Tensor)")
+def moe_align_quant(topk_ids, x, num_experts, block_m):
+    """moe_align(topk_ids) and fp8_quant_group128(x) in one call: (sorted_ids,
+    expert_ids, num_post_padded, qx, sx), the same bits as the two ops; up to
+    1024 slots and 64 tokens it is one kernel launch."""
+    _check(topk_ids.dtype == torch.int32 and topk_ids.is_contiguous(), "topk_ids must be contiguous int32")
+    _rowmajor(x, "x")
+    t, k = x.shape
+    _check(topk_ids.dim() == 2 and topk_ids.size(0) == t, "topk_ids must be [T, top_k] with one row per token of x")
+    n = topk_ids.numel()
+    cap, nblk = align_capacity(n, num_experts, block_m)
+    dev = topk_ids.device
+    sorted_ids = torch.empty((cap,), dtype=torch.int32, device=dev)
+    expert_ids = torch.empty((nblk,), dtype=torch.int32, device=dev)
+    num_post = torch.empty((1,), dtype=torch.int32, device=dev)
+    q = torch.empty((t, k), dtype=torch.float8_e4m3fn, device=dev)
+    s = torch.empty((t, k // 128), dtype=torch.float32, device=dev)
+    ws_bytes = _lib.query("strix_moe_align_workspace_bytes", n, num_experts)
+    ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev)
+    _lib.call("strix_moe_align_quant", _ptr(topk_ids), n, num_experts, block_m, _ptr(sorted_ids), cap,
+              _ptr(expert_ids), nblk, _ptr(num_post), _ptr(ws), ws_bytes, _ptr(x), _act_code(x), x.stride(0), _ptr(q),
+              k, _ptr(s), max(k // 128, 1), t, k, _stream(topk_ids))
+    return sorted_ids, expert_ids, num_post, q, s
+
+
+@_fake("moe_align_quant")
+def _(topk_ids, x, num_experts, block_m):
+    cap, nblk = align_capacity(topk_ids.numel(), num_experts, block_m)
+    return (topk_ids.new_empty((cap,)), topk_ids.new_empty((nblk,)), topk_ids.new_empty((1,)),
+            x.new_empty(x.shape, dtype=torch.float8_e4m3fn), x.new_empty((x.size(0), x.size(1) // 128),
+                                                                         dtype=torch.float32))
+
+
 # Extension: the router and the align as one op (up to 16 tokens and 1024
 # slots it runs as one single-block kernel); same outputs as moe_route_topk
 # then moe_align.

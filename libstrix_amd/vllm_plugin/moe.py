@@ -118,11 +118,13 @@ def _act(activation) -> str:
 
 
 def _chain(output, hidden_states, topk_weights, topk_ids, num_experts, n13, k_out, bm, apply_router_weight_on_input,
-           workspace13, workspace2, w13_call, w2_call, inter_dtype=None):
-    """align -> w13 (act*mul fused) -> w2 (x top-k weight) -> sum over top-k."""
+           workspace13, workspace2, w13_call, w2_call, inter_dtype=None, routed=None):
+    """align -> w13 (act*mul fused) -> w2 (x top-k weight) -> sum over top-k.
+    `routed` is an align already done by the caller (sorted_ids, expert_ids,
+    num_post_padded)."""
     t = hidden_states.size(0)
     top_k = topk_ids.size(1)
-    sorted_ids, expert_ids, num_post = _route(topk_ids, num_experts, bm)
+    sorted_ids, expert_ids, num_post = routed if routed is not None else _route(topk_ids, num_experts, bm)
     slots = t * top_k
     cache2 = _buf(workspace13, (slots, n13 // 2), inter_dtype or hidden_states.dtype, hidden_states.device)
     w13_call(cache2, sorted_ids, expert_ids, num_post, top_k)
@@ -162,9 +164,13 @@ def fp8_experts(output, hidden_states, w1, w2, s1, s2, topk_weights, topk_ids, a
     t, top_k = hidden_states.size(0), topk_ids.size(1)
     act = _act(activation)
     block = s1.dim() == 3 and s1.size(2) != 1
+    routed = None
     if block and w8a8:
         bm, bn = fp8_blocks(t, top_k, e)[0], _block_n(n13, k_out)
-        qx, sx = S.fp8_quant_group128(hidden_states.contiguous())
+        # The align and the activation quant in one call (one launch for decode).
+        ids = topk_ids if topk_ids.dtype == torch.int32 and topk_ids.is_contiguous() else \
+            topk_ids.to(torch.int32).contiguous()
+        *routed, qx, sx = S.moe_align_quant(ids, hidden_states.contiguous(), e, bm)
 
         def g13(c, si, ei, npp, k):
             S.moe_gemm_fp8_w8a8(c, qx, sx, w1, s1, si, ei, npp, None, k, bm, bn, True, act)
@@ -183,7 +189,7 @@ def fp8_experts(output, hidden_states, w1, w2, s1, s2, topk_weights, topk_ids, a
             S.moe_gemm_fp8(c, a, w2, s2, si, ei, npp, wts, 1, bm, bn, False, "silu")
 
     return _chain(output, hidden_states, topk_weights, topk_ids, e, n13, k_out, bm, apply_router_weight_on_input,
-                  workspace13, workspace2, g13, g2, inter_dtype=torch.bfloat16)
+                  workspace13, workspace2, g13, g2, inter_dtype=torch.bfloat16, routed=routed)
 
 
 def wna16_experts(output, hidden_states, w1, w2, s1, s2, topk_weights, topk_ids, group: int, activation="silu",

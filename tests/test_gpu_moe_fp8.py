@@ -228,3 +228,18 @@ def test_route_align_quant_matches_separate_ops(t, xdtype):
         if a.dtype == torch.float8_e4m3fn:
             a, b = a.view(torch.uint8), b.view(torch.uint8)
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("t", [1, 37, 64, 65, 128, 200])
+def test_align_quant_matches_separate_ops(t):
+    # Up to 1024 slots and 64 tokens the single-block align also quantizes the
+    # tokens; above, the separate kernels run. The same bits either way.
+    g = torch.Generator().manual_seed(200 + t)
+    ids = torch.stack([torch.randperm(128, generator=g)[:8] for _ in range(t)]).to(torch.int32).to(DEV)
+    x = (torch.randn(t, 2048, generator=g) * 2).to(torch.bfloat16).to(DEV)
+    got = torch.ops.strix.moe_align_quant(ids, x, 128, 16)
+    want = torch.ops.strix.moe_align(ids, 128, 16) + torch.ops.strix.fp8_quant_group128(x)
+    for a, b in zip(got, want):
+        if a.dtype == torch.float8_e4m3fn:
+            a, b = a.view(torch.uint8), b.view(torch.uint8)
+        assert torch.equal(a, b)

@@ -54,6 +54,9 @@ _OUT = {
     "w4a16_wmma_gemm": lambda x, w, s, b, g: torch.zeros(x.size(0), w.size(0), dtype=torch.bfloat16),
     "moe_align": lambda ids, e, bm: (torch.zeros(64, dtype=torch.int32), torch.zeros(4, dtype=torch.int32),
                                      torch.zeros(1, dtype=torch.int32)),
+    "moe_align_quant": lambda ids, x, e, bm: (torch.zeros(64, dtype=torch.int32), torch.zeros(4, dtype=torch.int32),
+                                              torch.zeros(1, dtype=torch.int32), torch.zeros(x.shape),
+                                              torch.ones(x.size(0), x.size(1) // 128)),
 }
 
 
@@ -332,10 +335,10 @@ def test_fp8_chain_order_and_flags(rec):
     s1 = torch.ones(e, 2 * inter // 128, h // 128)
     s2 = torch.ones(e, h // 128, inter // 128)
     out = moe.fp8_experts(None, x, w1, w2, s1, s2, w, ids, "gelu_tanh")
-    assert rec.calls == ["fp8_quant_group128", "moe_align", "moe_gemm_fp8_w8a8", "fp8_quant_group128",
+    assert rec.calls == ["moe_align_quant", "moe_gemm_fp8_w8a8", "fp8_quant_group128",
                          "moe_gemm_fp8_w8a8", "moe_sum"]
-    assert rec.args[1][0].dtype == torch.int32                     # ids handed to moe_align as int32
-    g13, g2 = rec.args[2], rec.args[4]
+    assert rec.args[0][0].dtype == torch.int32                     # ids handed to the align as int32
+    g13, g2 = rec.args[1], rec.args[3]
     assert g13[8] is None and g13[9] == 2 and g13[-2:] == (True, "gelu_tanh")     # top_k rows, fused act*mul
     assert torch.equal(g2[8], w.reshape(-1)) and g2[9] == 1 and g2[-2] is False   # top-k weight in w2
     assert g13[10] == moe.fp8_blocks(3, 2, 4)[0] and g13[11] == 128
