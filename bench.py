@@ -225,9 +225,11 @@ def point_c1(torch, S, timer):
     us_op = timer(op, iters=3 * len(sets))
     by = n * k + n * 4 + m * k * 2 + m * n * 2
     ops = 2.0 * m * n * k
-    return {"M": m, "gemm_us": round(us_k, 2), "op_us": round(us_op, 2), "gbs": round(by / us_k / 1e3, 1),
-            "frac_hbm": round(by / us_k / 1e3 / PEAK_HBM_GBS, 4), "tops": round(ops / us_k / 1e6, 2),
-            "cold_weight_sets": len(sets)}
+    us_graph = graph_us(torch, [lambda w=w, sw=sw: S.w8a8_scaled_mm(*S.int8_quant_per_token(x), w, sw)
+                                for (w, sw) in sets])
+    return {"M": m, "gemm_us": round(us_k, 2), "op_us": round(us_op, 2), "op_graph_us": round(us_graph, 2),
+            "gbs": round(by / us_k / 1e3, 1), "frac_hbm": round(by / us_k / 1e3 / PEAK_HBM_GBS, 4),
+            "tops": round(ops / us_k / 1e6, 2), "cold_weight_sets": len(sets)}
 
 
 def moe_bytes_fp8(ids, e_h, e_i, t, h, n_experts):
