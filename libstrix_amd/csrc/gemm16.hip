@@ -93,17 +93,27 @@ __device__ __forceinline__ float wscale(const G16& p, int e, int n, int k) {
 __device__ __forceinline__ int64_t wscale_row(const G16& p, int e, int n) {
   return (int64_t)e * p.ws_es + (int64_t)(n / p.ws_nblock) * p.ws_ns;
 }
+// The scale encoding: fixed by the format for MXFP4 (e8m0), else the runtime
+// kind. A compile-time kind keeps the streaming loops free of branches that
+// would make the compiler drain every outstanding load at the loop head.
+template <int FMT>
+__device__ __forceinline__ int scale_kind(const G16& p) {
+  if constexpr (FMT == kWMxfp4) return kSE8m0;
+  else return p.ws_kind;
+}
+template <int FMT>
 __device__ __forceinline__ uint32_t wscale_raw(const G16& p, int64_t row_idx, int k) {
   const int64_t idx = row_idx + (p.ws_kgroup ? (int64_t)(k / p.ws_kgroup) * p.ws_ks : 0);
-  switch (p.ws_kind) {
+  switch (scale_kind<FMT>(p)) {
     case kSF32: return static_cast<const uint32_t*>(p.ws)[idx];
     case kSBf16:
     case kSF16: return static_cast<const uint16_t*>(p.ws)[idx];
     default: return static_cast<const uint8_t*>(p.ws)[idx];
   }
 }
+template <int FMT>
 __device__ __forceinline__ float wscale_value(const G16& p, uint32_t raw) {
-  switch (p.ws_kind) {
+  switch (scale_kind<FMT>(p)) {
     case kSF32: return __uint_as_float(raw);
     case kSBf16: return bf16_bits_to_f32(raw);
     case kSF16: return f16_bits_to_f32(raw);
@@ -296,6 +306,23 @@ __global__ void __launch_bounds__(WAVES * 64) stream16_kernel(G16 p) {
             acc[s][t] = mfma_bf16(__builtin_bit_cast(bf16x8, wq), __builtin_bit_cast(bf16x8, av[t][j]), acc[s][t]);
         }
   };
+  const int skind = scale_kind<FMT>(p);
+  const int sbytes = skind == kSF32 ? 4 : (skind == kSE8m0 ? 1 : 2);
+  const uint32_t smask = sbytes == 4 ? 0xffffffffu : (sbytes == 2 ? 0xffffu : 0xffu);
+  // Pointer arithmetic (not integer casts) keeps the loads global, not flat.
+  auto word_at = [](const void* base, int64_t byte_off, uint32_t& word, uint32_t& shift) {
+    const uint8_t* b8 = static_cast<const uint8_t*>(base);
+    const int64_t mis = (int64_t)(reinterpret_cast<uintptr_t>(b8) & 3u);
+    const int64_t o = byte_off + mis;
+    word = *reinterpret_cast<const uint32_t*>(b8 + ((o & ~(int64_t)3) - mis));
+    shift = (uint32_t)(o & 3) * 8u;
+  };
+  // Scale bits -> value without a branch on the kind.
+  auto scale_of = [&](uint32_t raw) {
+    const float f32 = __uint_as_float(raw), bf = __uint_as_float(raw << 16), e8 = __uint_as_float(raw << 23);
+    const float h = f16_bits_to_f32(raw & 0xffffu);
+    return skind == kSF32 ? f32 : skind == kSBf16 ? bf : skind == kSF16 ? h : e8;
+  };
   constexpr bool HAS_S = (FMT != kWBf16);
   constexpr bool ZP = (FMT == kWInt4Zp);
   int64_t srow[NT], zrow[NT];
@@ -312,14 +339,14 @@ __global__ void __launch_bounds__(WAVES * 64) stream16_kernel(G16 p) {
       if constexpr (FMT == kWMxfp4 && !F16) {
         // e8m0 scales: bf16 by table (v_perm), the scalar path only for the
         // rare exponents the table cannot take. A lane's dwords share a scale.
-        if (p.ws_kind == kSE8m0 && mxfp4_lut_ok(sbits)) {
+        if (scale_kind<FMT>(p) == kSE8m0 && mxfp4_lut_ok(sbits)) {
           const Mxfp4Lut t = mxfp4_lut(sbits);
 #pragma unroll
           for (int i = 0; i < ndw; ++i) mxfp4_dword_lut(raw[i], t, &wv[4 * i]);
           return;
         }
       }
-      const float sc = wscale_value(p, sbits);
+      const float sc = scale_of(sbits);
       const float z = ZP ? (float)((wrow[s] & 1) ? ((zbits >> 4) & 15u) : (zbits & 15u)) : 8.0f;
       constexpr int PAIRS_PER_DWORD = 32 / BITS / 2;
 #pragma unroll
@@ -331,9 +358,20 @@ __global__ void __launch_bounds__(WAVES * 64) stream16_kernel(G16 p) {
   // decoded and multiplied. Every load is issued unconditionally (the index
   // is clamped to the wave's last chunk), so each wait counts exactly the
   // loads of the later chunk.
+  //
+  // Scales and zero points arrive as the aligned 32-bit word that holds
+  // them, whatever their width (f32, bf16/fp16, e8m0 or zero-point byte),
+  // with the bit offset kept beside it: one load form for every scale kind,
+  // so the loop has no branch on the kind (the compiler drains all
+  // outstanding loads at such a branch), and nothing narrower than a word is
+  // carried around the loop (a zero-extended copy would be computed at the
+  // loop latch, which would then wait for the chunk just issued). The word
+  // lies in the same 4-byte-aligned span as the element, so within the
+  // element's page.
   struct Buf {
     uint32_t w[NT][4];
     uint32_t s[NT], z[NT];
+    uint32_t ssh[NT], zsh[NT];
     u32x4 a[MT][PV / 8];
   };
   auto load = [&](int c, Buf& b) {
@@ -343,8 +381,11 @@ __global__ void __launch_bounds__(WAVES * 64) stream16_kernel(G16 p) {
       const u32x4 r4 = ldg128(wbase + (int64_t)wrow[s] * p.ldw + (int64_t)kc * BITS / 8);
 #pragma unroll
       for (int i = 0; i < 4; ++i) b.w[s][i] = r4[i];
-      if constexpr (HAS_S) b.s[s] = wscale_raw(p, srow[s], kc);
-      if constexpr (ZP) b.z[s] = wzero_raw(p, zrow[s], kc);
+      if constexpr (HAS_S) {
+        const int64_t si = srow[s] + (p.ws_kgroup ? (int64_t)(kc / p.ws_kgroup) * p.ws_ks : 0);
+        word_at(p.ws, si * sbytes, b.s[s], b.ssh[s]);
+      }
+      if constexpr (ZP) word_at(p.wz, zrow[s] + (int64_t)(kc / p.ws_kgroup) * p.wz_ks, b.z[s], b.zsh[s]);
     }
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
@@ -356,20 +397,27 @@ __global__ void __launch_bounds__(WAVES * 64) stream16_kernel(G16 p) {
   auto compute = [&](const Buf& b) {
     uint32_t wv[NT][PV / 2];
 #pragma unroll
-    for (int s = 0; s < NT; ++s) decode(b.w[s], 4, s, HAS_S ? b.s[s] : 0u, ZP ? b.z[s] : 0u, wv[s]);
+    for (int s = 0; s < NT; ++s) {
+      const uint32_t sbits = HAS_S ? (b.s[s] >> b.ssh[s]) & smask : 0u;
+      decode(b.w[s], 4, s, sbits, ZP ? (b.z[s] >> b.zsh[s]) & 0xffu : 0u, wv[s]);
+    }
     mfmas(wv, b.a, std::integral_constant<int, PV / 8>{});
   };
   const int f1 = min(c1, nfull);
   if (c0 < f1) {
+    // One exit, at the loop test: a break between the two halves makes the
+    // structurized loop carry a path on which B's loads are still pending at
+    // the loop head, and the compiler then drains every load there.
     Buf A, B;
     load(c0, A);
-    for (int c = c0; c < f1; c += 2) {
-      load(min(c + 1, f1 - 1), B);
+    int c = c0;
+    for (; c + 1 < f1; c += 2) {
+      load(c + 1, B);
       compute(A);
-      if (c + 1 >= f1) break;
       load(min(c + 2, f1 - 1), A);
       compute(B);
     }
+    if (c < f1) compute(A);
   }
   // A 4-bit K that is 64 mod 128 ends with a half chunk (8 bytes per lane).
   if constexpr (FMT != kWBf16 && BITS == 4) {
@@ -380,7 +428,7 @@ __global__ void __launch_bounds__(WAVES * 64) stream16_kernel(G16 p) {
       for (int s = 0; s < NT; ++s) {
         const uint2 r2 = *reinterpret_cast<const uint2*>(wbase + (int64_t)wrow[s] * p.ldw + (int64_t)kc * BITS / 8);
         const uint32_t raw[2] = {r2.x, r2.y};
-        decode(raw, 2, s, wscale_raw(p, srow[s], kc), ZP ? wzero_raw(p, zrow[s], kc) : 0u, wv[s]);
+        decode(raw, 2, s, wscale_raw<FMT>(p, srow[s], kc), ZP ? wzero_raw(p, zrow[s], kc) : 0u, wv[s]);
       }
       u32x4 av[MT][PV / 8];
 #pragma unroll
@@ -562,7 +610,7 @@ __global__ void __launch_bounds__((WM * WN + NP) * 64) tiled16_kernel(G16 p, int
     for (int j = 0; j < PPT; ++j) {
       const int k = kb * 64 + pidx[j] * PV;
       b.w[j] = ldg128(wbase + (int64_t)pgrow[j] * p.ldw + (int64_t)k * BITS / 8);
-      if constexpr (!DIRECT_W) b.s[j] = wscale_raw(p, srow[j], k);
+      if constexpr (!DIRECT_W) b.s[j] = wscale_raw<FMT>(p, srow[j], k);
       if constexpr (ZP) b.z[j] = wzero_raw(p, zrow[j], k);
     }
   };
@@ -579,12 +627,12 @@ __global__ void __launch_bounds__((WM * WN + NP) * 64) tiled16_kernel(G16 p, int
     uint8_t* st = smem + buf * STAGE;
 #pragma unroll
     for (int j = 0; j < PPT; ++j) {
-      const float sc = wscale_value(p, b.s[j]);
+      const float sc = wscale_value<FMT>(p, b.s[j]);
       const float z = ZP ? (float)((pgrow[j] & 1) ? (b.z[j] >> 4) : (b.z[j] & 15)) : 8.0f;
       uint32_t v[PV / 2];
       constexpr int PAIRS_PER_DWORD = 32 / BITS / 2;
       if constexpr (FMT == kWMxfp4 && !F16) {
-        if (p.ws_kind == kSE8m0 && mxfp4_lut_ok(b.s[j])) {
+        if (scale_kind<FMT>(p) == kSE8m0 && mxfp4_lut_ok(b.s[j])) {
           const Mxfp4Lut t = mxfp4_lut(b.s[j]);
 #pragma unroll
           for (int i = 0; i < 4; ++i) mxfp4_dword_lut(b.w[j][i], t, &v[4 * i]);
@@ -741,7 +789,7 @@ __global__ void __launch_bounds__(256) dequant_kernel(G16 p, uint16_t* out, int6
   constexpr int PAIRS_PER_DWORD = 32 / BITS / 2;
   bool done = false;
   if constexpr (FMT == kWMxfp4) {
-    const uint32_t b = p.ws_kind == kSE8m0 ? wscale_raw(p, wscale_row(p, 0, n), k) : 1u;
+    const uint32_t b = p.ws_kind == kSE8m0 ? wscale_raw<FMT>(p, wscale_row(p, 0, n), k) : 1u;
     if (p.ws_kind == kSE8m0 && mxfp4_lut_ok(b)) {
       const Mxfp4Lut t = mxfp4_lut(b);
 #pragma unroll
