@@ -33,6 +33,7 @@ PEAK_BF16_TFLOPS = 2500.0  # MI355X dense BF16
 PEAK_INT8_TOPS = 5000.0
 PEAK_HBM_GBS = 8000.0
 MALL_BYTES = 256 << 20
+HEADLINE_WARM_S = 0.1  # warm-up floor of the headline step loop (seconds)
 
 
 def log(msg: str) -> None:
@@ -116,9 +117,19 @@ def headline(torch, S, timer, steps, warmup):
         q, s = S.fp8_quant_group128(x)
         return S.fp8_w8a8_block_gemm(q, s, w, sw)
 
-    for _ in range(warmup):
+    # Warm up for `warmup` steps and at least HEADLINE_WARM_S seconds, the
+    # same rule as Timer: the clock settles only after some tens of ms of
+    # sustained MFMA load, and a step-count warm-up alone (the driver passes
+    # --warmup 5) would time the clock dip instead of the steady state.
+    t_warm = time.perf_counter()
+    n_warm = 0
+    while n_warm < warmup or time.perf_counter() - t_warm < HEADLINE_WARM_S:
         step(0)
+        n_warm += 1
+        if n_warm % 8 == 0:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
+    warm_ms = (time.perf_counter() - t_warm) * 1e3
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     t0.record()
@@ -136,6 +147,7 @@ def headline(torch, S, timer, steps, warmup):
     return {
         "ms_per_step": ms_step,
         "value": value,
+        "warmup_run": {"steps": n_warm, "ms": round(warm_ms, 1)},
         "gemm_us": us_gemm,
         "roofline": {
             "bound": "mfma",
@@ -285,29 +297,104 @@ def point_moe16(torch, S, timer, name, t, d, run, bytes_per_expert, e, top_k, h,
     return res
 
 
+def _cpu_model() -> str:
+    """The host CPU's model name (lscpu's "Model name", read from /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or "unknown"
+
+
+def _median_s(fn, runs: int = 3) -> float:
+    """One untimed warm-up call, then the median of `runs` timed calls (seconds)."""
+    fn()
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return sorted(times)[len(times) // 2]
+
+
 def cpu_baseline(torch):
-    """The oracle's dequantize-then-fp32-matmul on the host, config 2 weights,
-    a sample of 128 activation rows (full weight dequant each call, as the
-    reference's torch path does)."""
+    """The oracle's dequantize-then-fp32-matmul restatement of each config on
+    the host cores (kind "port"), on the same seeded inputs as the GPU points:
+    one warm-up, median of 3 per config. Samples are bounded so the leg stays
+    near 30 s of CPU work; each keeps the per-call work of the reference's
+    torch path (full weight dequant of every touched expert per call). The
+    top-level value is config 2's, the headline's config."""
     import oracle
     from libstrix_amd import workloads
 
     threads = min(len(os.sched_getaffinity(0)), int(os.environ.get("OMP_NUM_THREADS", "64")))
     torch.set_num_threads(threads)
+    res = {}
+
+    # Config 1: the whole M=32 call (per-token quant, exact int accumulate, epilogue).
+    d = workloads.c1_int8(seed=1)
+    m, k = d["x"].shape
+    n = d["w"].size(0)
+
+    def c1():
+        qa, sa = oracle.int8_quant_per_token(d["x"])
+        oracle.w8a8_int8_gemm(qa, sa, d["w"], d["sw"])
+
+    t = _median_s(c1)
+    res["c1_int8_dense"] = {"sample": f"M={m} N={n} K={k} (whole config)", "ms": round(t * 1e3, 2),
+                            "gflops": round(2.0 * m * n * k / t / 1e9, 2),
+                            "gbs": round((n * k + m * k * 2 + m * n * 2) / t / 1e9, 2)}
+
+    # Config 2: 128 of the 4096 activation rows (full weight dequant per call).
     m, n, k = 128, 17408, 5120
     d = workloads.c2_fp8(seed=2, m=m, n=n, k=k)
-    times = []
-    for it in range(3):
-        t0 = time.perf_counter()
+
+    def c2():
         qa, sa = oracle.fp8_quant_group128(d["x"])
         oracle.fp8_block_gemm(qa, sa, d["w"], d["sw"])
-        times.append(time.perf_counter() - t0)
-    t = sorted(times)[1]
-    flops = 2.0 * m * n * k
-    return {"value": round(flops / t / 1e9, 2), "unit": "GFLOP/s", "cores": threads, "kind": "port",
-            "sample": f"config 2 FP8-block W8A8, M={m} rows of 4096, N={n}, K={k}; act QDQ + full weight "
-                      f"dequant + fp32 matmul per call, median of 3 ({t * 1e3:.0f} ms)",
-            "seconds_per_call": round(t, 3)}
+
+    t2 = _median_s(c2)
+    res["c2_fp8_dense"] = {"sample": f"M={m} rows of 4096, N={n}, K={k}", "ms": round(t2 * 1e3, 2),
+                           "gflops": round(2.0 * m * n * k / t2 / 1e9, 2)}
+    del d
+
+    def moe_leg(name, t, e, top_k, h, inter, get13, get2, logits, x, act_quant):
+        ids, w = oracle.route_topk(logits[:t], top_k)
+        fn = lambda: oracle.fused_moe(x[:t], ids, w, get13, get2, act_quant=act_quant)
+        tm = _median_s(fn)
+        flops = 2.0 * t * top_k * (2 * inter * h + h * inter)
+        res[name] = {"sample": f"T={t} tokens (E={e}, top_k={top_k}, H={h}, I={inter}; "
+                               f"{int(ids.unique().numel())} experts dequantized per call)",
+                     "ms": round(tm * 1e3, 2), "gflops": round(flops / tm / 1e9, 2)}
+
+    c3 = workloads.c3_fp8_moe(seed=3, t=64)
+    moe_leg("c3_fp8_moe", 64, 128, 8, 2048, 768,
+            lambda e_: oracle.fp8_block_dequant(c3["w13"][e_], c3["w13_s"][e_]),
+            lambda e_: oracle.fp8_block_dequant(c3["w2"][e_], c3["w2_s"][e_]), c3["logits"], c3["x"], "fp8")
+    del c3
+    c4 = workloads.c4_mxfp4_moe(seed=4, t=2)
+    moe_leg("c4_mxfp4_moe", 2, 32, 4, 2880, 2880,
+            lambda e_: oracle.mxfp4_decode(c4["w13"][e_], c4["w13_s"][e_]),
+            lambda e_: oracle.mxfp4_decode(c4["w2"][e_], c4["w2_s"][e_]), c4["logits"], c4["x"], None)
+    del c4
+    c5 = workloads.c5_wna16_moe(seed=5, t=64)
+    moe_leg("c5_wna16_moe", 64, 128, 8, 2048, 768,
+            lambda e_: oracle.wna16_zp_decode(c5["w13"][e_], c5["w13_s"][e_], c5["w13_z"][e_], 128),
+            lambda e_: oracle.wna16_zp_decode(c5["w2"][e_], c5["w2_s"][e_], c5["w2_z"][e_], 128),
+            c5["logits"], c5["x"], None)
+    del c5
+
+    c2r = res["c2_fp8_dense"]
+    return {"value": c2r["gflops"], "unit": "GFLOP/s", "cores": threads, "cpu_model": _cpu_model(),
+            "kind": "port",
+            "sample": f"config 2 FP8-block W8A8, {c2r['sample']}; act QDQ + full weight dequant + fp32 matmul "
+                      f"per call, one warm-up then median of 3 ({c2r['ms']:.0f} ms)",
+            "configs": res}
 
 
 def traffic_from_profile():
@@ -358,6 +445,7 @@ def main() -> None:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "warmup_run": h["warmup_run"],
         "ms_per_step": round(h["ms_per_step"], 4),
         "higher_is_better": True,
         "scaling": "weak",

@@ -217,6 +217,19 @@ int strix_moe_align_quant(const int32_t* topk_ids, int64_t num_slots, int64_t E,
                           int32_t* num_post, void* workspace, int64_t workspace_bytes, const void* x, int x_dtype,
                           int64_t ldx, uint8_t* q, int64_t ldq, float* s, int64_t lds, int64_t T, int64_t K,
                           void* stream);
+/* strix_moe_align without a workspace argument and without any allocation:
+ * no counterpart in the reference. For callers that cannot allocate (code
+ * under HIP graph capture, serving loops that forbid hipMalloc). The
+ * histogram lives in a 1 MiB device array of the library (one per GPU, held
+ * until the process ends), so chunks * E <= 262144 with chunks =
+ * ceil(num_slots / 256) (e.g. 524288 slots at E = 128); larger inputs are
+ * rejected with an error. Calls that overlap on one GPU share the array and
+ * race. Same outputs as strix_moe_align, bit for bit.
+ * strix_moe_align_noalloc_max_bytes() returns the array's size. */
+int64_t strix_moe_align_noalloc_max_bytes(void);
+int strix_moe_align_noalloc(const int32_t* topk_ids, int64_t num_slots, int64_t E, int64_t block_m,
+                            int32_t* sorted_ids, int64_t sorted_cap, int32_t* expert_ids, int64_t blocks_cap,
+                            int32_t* num_post, void* stream);
 /* Router and align in one call: the reference runs vLLM's fused_topk then
  * moe_align_block_size (python/strix_vllm/moe.py:181-184, 286-288). Same
  * outputs as strix_moe_route_topk (ldo = top_k) followed by strix_moe_align;

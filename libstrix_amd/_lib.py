@@ -60,6 +60,8 @@ SIGNATURES: dict[str, list] = {
     "strix_moe_align_sorted_capacity": [L, L, L],
     "strix_moe_align_workspace_bytes": [L, L],
     "strix_moe_align": [P, L, L, L, P, L, P, L, P, P, L, P],
+    "strix_moe_align_noalloc_max_bytes": [],
+    "strix_moe_align_noalloc": [P, L, L, L, P, L, P, L, P, P],
     "strix_moe_align_quant": [P, L, L, L, P, L, P, L, P, P, L, P, I, L, P, L, P, L, L, L, P],
     "strix_moe_route_align": [P, I, L, L, L, L, I, P, P, L, P, L, P, L, P, P, L, P],
     "strix_moe_route_align_quant": [P, I, L, L, L, L, I, P, P, L, P, L, P, L, P, P, L, P, I, L, P, L, P, L, L, P],
@@ -72,6 +74,7 @@ _RESTYPE = {
     "strix_last_error": c_char_p,
     "strix_moe_align_sorted_capacity": c_int64,
     "strix_moe_align_workspace_bytes": c_int64,
+    "strix_moe_align_noalloc_max_bytes": c_int64,
 }
 
 _lib: ctypes.CDLL | None = None

@@ -32,6 +32,13 @@ inline bool aligned(const void* p, int bytes) {
   return (reinterpret_cast<uintptr_t>(p) % bytes) == 0;
 }
 
+// The tiled kernels address an operand's rows with 32-bit per-lane byte
+// offsets from a wave-uniform base: true when `rows` rows of `row_bytes`
+// bytes at a stride of `stride_bytes` all lie within 4 GiB of the first.
+inline bool fits_u32_rows(int64_t rows, int64_t stride_bytes, int64_t row_bytes) {
+  return rows <= 0 || (rows - 1) * stride_bytes + row_bytes <= (int64_t)UINT32_MAX;
+}
+
 }  // namespace strix
 
 // Validation helpers: return from the enclosing entry point with a message.

@@ -904,6 +904,10 @@ int run_moe16(const char* op, const MoeArgs& m, G16 p, void* stream) {
                 (long long)n_out);
   STRIX_REQUIRE(m.activation == kActSilu || m.activation == kActGeluTanh, "%s: unknown activation", op);
   STRIX_REQUIRE(aligned(p.w, 16) && p.ldw % 16 == 0, "%s: weight rows must be 16-byte aligned", op);
+  STRIX_REQUIRE(m.num_slots <= INT32_MAX && m.N <= INT32_MAX && m.K <= INT32_MAX, "%s: sizes overflow 32-bit indexing",
+                op);
+  STRIX_REQUIRE(fits_u32_rows(m.num_slots, m.lda * 2, m.K * 2) && fits_u32_rows(m.N, p.ldw, p.ldw),
+                "%s: an operand spans more than 4 GiB (the kernels use 32-bit row offsets); split the call", op);
   int rc = check_scale_kind(op, p.ws_kind);
   if (rc) return rc;
   if (m.num_blocks == 0 || m.num_slots == 0 || m.N == 0) return STRIX_OK;
@@ -937,6 +941,8 @@ int run_dense16(const char* op, G16 p, const void* x, int x_dtype, int64_t ldx, 
   STRIX_REQUIRE(ldo >= N && ldo % 4 == 0 && aligned(out, 8), "%s: output rows must be >= N, 8-byte aligned", op);
   STRIX_REQUIRE(aligned(p.w, 16) && p.ldw % 16 == 0, "%s: weight rows must be 16-byte aligned", op);
   STRIX_REQUIRE(M <= INT32_MAX && N <= INT32_MAX && K <= INT32_MAX, "%s: sizes overflow 32-bit indexing", op);
+  STRIX_REQUIRE(fits_u32_rows(M, ldx * 2, K * 2) && fits_u32_rows(N, p.ldw, p.ldw),
+                "%s: an operand spans more than 4 GiB (the kernels use 32-bit row offsets); split the call", op);
   int rc = check_scale_kind(op, p.ws_kind);
   if (rc) return rc;
   if (M == 0 || N == 0) return STRIX_OK;

@@ -1247,6 +1247,8 @@ int check_common(const char* op, int64_t M, int64_t N, int64_t K, int64_t lda, i
   STRIX_REQUIRE(lda >= K && lda % 16 == 0, "%s: activation row stride must be >= K and a multiple of 16", op);
   STRIX_REQUIRE(aligned(a, 16) && aligned(w, 16), "%s: operands must be 16-byte aligned", op);
   STRIX_REQUIRE(M <= INT32_MAX && N <= INT32_MAX && K <= INT32_MAX, "%s: sizes overflow 32-bit indexing", op);
+  STRIX_REQUIRE(fits_u32_rows(M, lda, K) && fits_u32_rows(N, ldw, K),
+                "%s: an operand spans more than 4 GiB (the kernels use 32-bit row offsets); split the call", op);
   return STRIX_OK;
 }
 

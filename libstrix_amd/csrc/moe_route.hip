@@ -11,6 +11,8 @@
 //   align:  stable counting sort of slot ids by expert: within an expert the
 //           slots appear in ascending order, each expert's run is padded to a
 //           multiple of block_m with the id S = T*top_k.
+#include <mutex>
+
 #include "capi_internal.h"
 #include "quant_common.h"
 #include "strix_common.h"
@@ -636,6 +638,71 @@ int strix_moe_align_quant(const int32_t* topk_ids, int64_t num_slots, int64_t E,
   STRIX_REQUIRE(T >= 0 && T <= num_slots, "%s: bad token count", op);
   return align_impl(op, topk_ids, num_slots, E, block_m, sorted_ids, sorted_cap, expert_ids, blocks_cap, num_post,
                     workspace, workspace_bytes, act, T, x_dtype, stream);
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------------ no-allocation align
+// The align's histogram workspace as a device array of the library, for
+// callers that cannot allocate (HIP graph capture, serving loops). Each GPU
+// holds its own copy for the life of the process. Every call on a GPU shares
+// it, so calls that overlap on one GPU (different streams, different host
+// threads) race. Nothing in it must start at zero: pass 1 writes every
+// (chunk, expert) count before pass 2 reads it.
+namespace strix {
+namespace {
+
+constexpr int64_t kAlignScratchBytes = int64_t(1) << 20;  // 1 MiB: chunks(num_slots) * E <= 262144
+__device__ __align__(256) int32_t scratch[kAlignScratchBytes / 4];
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[64] = {};  // device address of `scratch` per device, set on first use
+
+// Device address of this device's `scratch` (looked up once per device, with
+// that device current). In host code the array's name is only a stand-in, so
+// kernels always receive this address.
+int align_scratch(void** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+    return set_error(STRIX_ERR_DEVICE, "moe_align_noalloc: no usable current HIP device");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr)
+      return set_error(STRIX_ERR_DEVICE, "moe_align_noalloc: hipGetSymbolAddress(scratch) failed: %s",
+                       hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return STRIX_OK;
+}
+
+}  // namespace
+}  // namespace strix
+
+extern "C" {
+
+int64_t strix_moe_align_noalloc_max_bytes(void) { return strix::kAlignScratchBytes; }
+
+int strix_moe_align_noalloc(const int32_t* topk_ids, int64_t num_slots, int64_t E, int64_t block_m,
+                            int32_t* sorted_ids, int64_t sorted_cap, int32_t* expert_ids, int64_t blocks_cap,
+                            int32_t* num_post, void* stream) {
+  const char* op = "moe_align_noalloc";
+  STRIX_REQUIRE(E >= 1 && E <= 1024, "%s: 1 <= E <= 1024, got %lld", op, (long long)E);
+  STRIX_REQUIRE(num_slots >= 0 && num_slots < INT32_MAX / 2, "%s: bad slot count", op);
+  const int64_t need = strix_moe_align_workspace_bytes(num_slots, E);
+  STRIX_REQUIRE(need <= strix::kAlignScratchBytes,
+                "%s: %lld slots x %lld experts need %lld bytes of histogram, over the %lld-byte static scratch; "
+                "use strix_moe_align with a workspace",
+                op, (long long)num_slots, (long long)E, (long long)need, (long long)strix::kAlignScratchBytes);
+  STRIX_ARCH_GATE();
+  void* ws = nullptr;
+  int rc = strix::align_scratch(&ws);
+  if (rc) return rc;
+  const strix::ActQuant none = {};
+  return strix::align_impl(op, topk_ids, num_slots, E, block_m, sorted_ids, sorted_cap, expert_ids, blocks_cap,
+                           num_post, ws, strix::kAlignScratchBytes, none, 0, STRIX_BF16, stream);
 }
 
 }  // extern "C"

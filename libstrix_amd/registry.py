@@ -402,6 +402,15 @@ KERNELS: list[Kernel] = [
         {"kernel": "stream16 (M <= 32 path of strix_w16_gemm)"},
     ),
     Kernel(
+        "w8a16_gemm",
+        "w8a16",
+        "the same uint8b128 W8A16 contraction at any M (bf16/fp16 activations as given, weights decoded "
+        "exactly): the prefill path of layers whose 32/64-element groups the W8A8 op does not take. "
+        "K % 64 == 0",
+        {"weight_bits": 8, "group_size": (0, 32, 64, 128), "dtype": ("bf16", "fp16")},
+        {"kernel": "stream16 to 64 rows, tiled16 above"},
+    ),
+    Kernel(
         "fp8_skinny_gemm",
         "fp8",
         "decode GEMM (M <= 8) on float8_e4m3fn weights with fp32 scales per (row, 128-K block) [N, K/128] or "

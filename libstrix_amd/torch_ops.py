@@ -1048,6 +1048,38 @@ def _(in_a, in_b, in_scale, in_bias, CuCount, group_size):
     return in_b.new_empty((in_b.size(0), in_a.size(0)))
 
 
+# New op (no reference schema): the same uint8b128 W8A16 contraction at any
+# M, for the group sizes the W8A8 op does not take (32, 64). Bf16/fp16
+# activations are used as given; weights are decoded exactly in registers
+# (M <= 64) or LDS (larger M) and contracted with 16-bit MFMA.
+@_define("w8a16_gemm(Tensor in_a, Tensor in_b, Tensor in_scale, Tensor? in_bias, int group_size) -> Tensor")
+def w8a16_gemm(in_a, in_b, in_scale, in_bias, group_size):
+    _check(in_a.dim() == 2 and in_b.dim() == 2, "Weights must be [N, K] and activations [M, K]")
+    _check(in_a.dtype == torch.uint8, f"Weights must be uint8 (uint8b128), got {in_a.dtype}")
+    _check(in_b.dtype in (torch.float16, torch.bfloat16), "Activation must be float16 or bfloat16")
+    _check(in_scale.dtype == in_b.dtype, "Scale dtype must match activation dtype")
+    _check(group_size in (0, 32, 64, 128), f"group_size must be 0 (per-channel), 32, 64, or 128, got {group_size}")
+    n, k = in_a.shape
+    _check(in_b.size(1) == k and in_b.stride(1) == 1 and in_a.stride(1) == 1, "K mismatch or non-contiguous rows")
+    _check(k % 64 == 0, f"K must be a multiple of 64, got K={k}")
+    if group_size:
+        _check(k % group_size == 0, f"K must be divisible by group_size={group_size}")
+        _check(in_scale.dim() == 2 and tuple(in_scale.shape) == (n, k // group_size) and in_scale.stride(1) == 1,
+               f"Scale must be [{n}, {k // group_size}] but got {list(in_scale.shape)}")
+        s_ns, s_ks = in_scale.stride(0), 1
+    else:
+        _check(in_scale.numel() == n, f"Per-channel scale must be [{n}]")
+        in_scale = in_scale.reshape(-1).contiguous()
+        s_ns, s_ks = 1, 0
+    return _w16(_lib.FMT_U8B128, in_a, in_b, in_scale, _SCALE_KIND[in_scale.dtype], s_ns, s_ks, group_size, 1,
+                in_bias)
+
+
+@_fake("w8a16_gemm")
+def _(in_a, in_b, in_scale, in_bias, group_size):
+    return in_b.new_empty((in_b.size(0), in_a.size(0)))
+
+
 # Reference schema: csrc/torch_ops.cpp:253-255: e4m3 weights, fp32 scales per
 # row [N] or per (row, 128-K block) [N, K/128].
 @_define(

@@ -11,7 +11,7 @@ Environment, as in the reference (python/strix_vllm/__init__.py:18-24):
   STRIX_DISABLE=all, or a comma list of swap names, keeps vLLM's own kernels
   for those swaps. Names: w8a8, fp8, fp8_channel, fp8_w8a8, mxfp4, w8a16,
   w4a16, moe_gemm, moe_pad, moe_w4a16, moe_fp8, moe_fp8_w8a8, moe_w8a16,
-  moe_w4a8.
+  moe_w4a8, moe_mxfp4.
   STRIX_ENABLE=<names> turns on the opt-in swaps (ARCH_GATED) for any model.
 
 The modules split as in the reference: `int8` (W8A8 int8 linears), `fp8`
@@ -59,22 +59,24 @@ def enabled(op: str) -> bool:
 
 
 def _model_architectures() -> list[str]:
-    """Architectures of the model being loaded; [] outside a vLLM config or
-    without vLLM (python/strix_vllm/__init__.py:62-75)."""
+    """Names the model being loaded goes by: its HF `architectures` list and
+    vLLM's resolved architecture, without repeats. Empty without vLLM or
+    outside a model load (the role of python/strix_vllm/__init__.py:62-75)."""
     try:
         from vllm.config import get_current_vllm_config_or_none
     except ImportError:
         return []
-    config = get_current_vllm_config_or_none()
-    model_config = getattr(config, "model_config", None)
-    if model_config is None:
+    mc = getattr(get_current_vllm_config_or_none(), "model_config", None)
+    if mc is None:
         return []
-    archs = list(getattr(model_config.hf_config, "architectures", None) or [])
-    try:
-        archs.append(model_config.architecture)
-    except Exception:
-        pass
-    return archs
+    names = [*(getattr(getattr(mc, "hf_config", None), "architectures", None) or [])]
+    resolved = getattr(type(mc), "architecture", None)
+    if resolved is not None:
+        try:
+            names.append(mc.architecture)
+        except (AttributeError, ValueError, RuntimeError):
+            pass   # vLLM could not resolve one; the HF names stand
+    return list(dict.fromkeys(n for n in names if isinstance(n, str)))
 
 
 def model_gate(op: str, archs: list[str] | None = None) -> bool:
@@ -98,17 +100,26 @@ def on_gfx950() -> bool:
 
 
 def _cache_factor(active: bool) -> str:
-    """Digest of whether the plugin is active, STRIX_DISABLE, STRIX_ENABLE and
-    the plugin's own sources (python/strix_vllm/__init__.py:119-134): the
-    dispatchers run inside code torch.compile traces, and vLLM keys its
-    compile caches on its own configuration only, so a graph traced with the
-    plugin off (or an older plugin) must not be replayed with it on."""
-    h = hashlib.sha256(b"active" if active else b"inactive")
-    h.update(os.environ.get("STRIX_DISABLE", "").encode())
-    h.update(os.environ.get("STRIX_ENABLE", "").encode())
-    for f in sorted(Path(__file__).parent.glob("*.py")):
-        h.update(f.read_bytes())
-    return h.hexdigest()[:16]
+    """A short key for vLLM's compile caches. The dispatchers run inside code
+    torch.compile traces, and vLLM keys its caches on its own configuration
+    only, so a graph traced with the plugin off, under other STRIX_* settings,
+    or with other op wrappers must not be replayed. The key covers exactly
+    those inputs: the activity flag, the two environment lists (as sorted
+    sets, so order and spacing do not matter) and the source text of the
+    plugin modules and of the torch op layer they call (the role of
+    python/strix_vllm/__init__.py:119-134)."""
+    import json
+
+    pkg = Path(__file__).resolve().parent
+    sources = sorted(pkg.glob("*.py")) + [pkg.parent / "torch_ops.py"]
+    state = {
+        "active": bool(active),
+        "disable": sorted(_env_names("STRIX_DISABLE")),
+        "enable": sorted(_env_names("STRIX_ENABLE")),
+        "sources": {f.name: hashlib.blake2b(f.read_bytes(), digest_size=16).hexdigest()
+                    for f in sources if f.exists()},
+    }
+    return hashlib.blake2b(json.dumps(state, sort_keys=True).encode(), digest_size=8).hexdigest()
 
 
 def register() -> None:

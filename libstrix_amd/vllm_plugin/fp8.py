@@ -123,11 +123,21 @@ def prepare_block(w: torch.Tensor, block_scale: torch.Tensor, kmajor: bool = Fal
 
 def prepare_channel(w: torch.Tensor, s: torch.Tensor, n: int) -> tuple[torch.Tensor, torch.Tensor]:
     """Per-channel load transform (python/strix_vllm/fp8.py:222-241): the
-    weight may arrive as a [K, N] view; rows are made [N, K], scales fp32 [N]."""
+    weight may arrive as a [K, N] view; rows are made [N, K], scales fp32 [N].
+
+    The orientation is read from the strides, not the sizes, so square
+    weights (N == K) are handled: a column-major view (stride(0) == 1) is the
+    transpose of [N, K] rows. A row-major tensor is [N, K] when its first
+    size is N, else a stored [K, N] matrix."""
     if w.dtype != torch.float8_e4m3fn:
         raise RuntimeError(f"strix FP8 takes float8_e4m3fn, got {w.dtype}")
-    if w.size(0) != n:
+    if w.dim() != 2:
+        raise RuntimeError(f"strix FP8 per-channel weight must be 2-D, got {w.dim()}-D")
+    col_major = w.stride(0) == 1 and w.stride(1) != 1 and w.size(0) > 1
+    if col_major or w.size(0) != n:
         w = w.t()
+    if w.size(0) != n:
+        raise RuntimeError(f"per-channel weight {list(w.shape)} has no dimension of N={n} rows")
     w = w.contiguous()
     s = s.float().reshape(-1).contiguous()
     if s.numel() == 1:

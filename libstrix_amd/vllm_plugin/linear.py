@@ -1,25 +1,34 @@
 # SPDX-License-Identifier: MIT
 """W8A16 (compressed-tensors uint8b128) and W4A16 (uint4b8) linears on gfx950.
 
-W8A16 follows the reference (python/strix_vllm/linear.py:74-93): weights
-stored once as uint8 [N, K] (raw byte - 128 is the signed value); decode rows
-run `w8a16_skinny_gemm` (bf16 activations, exact weights), larger M runs
-`w8a8_wmma_gemm` (activations quantized per 128-element group inside the op,
-int8 MFMA) with the scales as fp32 [N] or [G, N], transposed once per weight
-and cached.
+W8A16 keeps the checkpoint's numerics (bf16/fp16 activations against exact
+weights) for decode and, like the reference (python/strix_vllm/linear.py:
+74-93), quantizes prefill activations per 128-element group onto the int8
+MFMA path. Weights are stored once as uint8 [N, K] (byte - 128 is the signed
+value). Everything the forward needs is prepared once at load by
+`prepare_w8`:
+
+- the raw scales in the checkpoint's [N] / [N, G] layout, read by the decode
+  and group-32/64 paths;
+- for per-channel and 128-group layers, an fp32 copy in the layout the W8A8
+  op reads ([N], or [G, N]), kept on the layer beside the weight. Other
+  group sizes have none and run W8A16 at every M on `w8a16_gemm`.
+
+Per forward: up to MAX_SKINNY_BATCH_SIZE rows `w8a16_skinny_gemm`; above,
+`w8a8_wmma_gemm` with the load-time fp32 scales, or `w8a16_gemm` when the
+layer has none.
 
 W4A16 takes the RDNAHybridW4A16 packed int4 words (python/strix_vllm/linear.py:
 100-137). The reference keeps decode on vLLM's own skinny int4 kernel and
 runs prefill as W4A8 (int8 activations) or, for 32-element groups, a bf16
 dequant tile. Here every M stays W4A16 (bf16 activations, exact weights):
 `w4a16_wmma_gemm` below DEQUANT_MIN_M rows, `w4a16_dequant` + hipBLASLt from
-there (51 vs 126 us at M=128, 463 vs 658 us at M=8192, N=K=5120, MI355X);
-W4A8 has no speed to offer on gfx950, where the bf16 path is the faster one.
+there (51 vs 126 us at M=128, 463 vs 658 us at M=8192, N=K=5120, MI355X).
 """
 
 from __future__ import annotations
 
-import weakref
+from typing import NamedTuple
 
 import torch
 
@@ -30,11 +39,18 @@ from libstrix_amd.vllm_plugin.mxfp4 import DEQUANT_MIN_M
 S = torch.ops.strix
 
 MAX_SKINNY_BATCH_SIZE = 8
-_W8A8_GROUP_SIZE = 128
-# fp32 W8A8 scale copies keyed by weight identity (python/strix_vllm/linear.py:
-# 27, 42-71); covers every quantized linear of a large model.
-_W8A8_PREP_MAX_ENTRIES = 1024
-_W8A8_PREP: dict[int, tuple[weakref.ref, torch.Tensor]] = {}
+W8A8_GROUP = 128  # the activation group of the W8A8 op; weight groups must match it (or be per channel)
+# Attribute holding the load-time W8A8 scales on a vLLM layer.
+W8A8_SCALE_ATTR = "strix_w8a8_scale"
+
+
+class W8Weights(NamedTuple):
+    """A W8A16 layer's tensors after loading."""
+
+    w_q: torch.Tensor            # uint8 [N, K], byte - 128 = signed value
+    w_s: torch.Tensor            # checkpoint scales: [N] per channel or [N, K/group]
+    w8a8_s: torch.Tensor | None  # fp32 [N] or [K/128, N] for w8a8_wmma_gemm; None = W8A16 at every M
+    group_size: int              # 0 = per channel
 
 
 def pack_w8_rows(unpacked: torch.Tensor) -> torch.Tensor:
@@ -42,47 +58,54 @@ def pack_w8_rows(unpacked: torch.Tensor) -> torch.Tensor:
     return (unpacked & 0xFF).to(torch.uint8).contiguous()
 
 
-def w8a8_scales(w_q: torch.Tensor, w_s: torch.Tensor, group_size: int) -> torch.Tensor | None:
-    """fp32 scales for the W8A8 op: [N] per channel, [G, N] for 128-element
-    groups; None when the layout is one the op does not take. Cached per
-    weight tensor (the weakref guards against a reused id)."""
-    n, k = w_q.shape
+def w8a8_scale_layout(w_s: torch.Tensor, n: int, k: int, group_size: int) -> torch.Tensor | None:
+    """The fp32 weight scales in the W8A8 op's layout: [N] per channel,
+    [K/128, N] for 128-element groups; None for any other grouping (or a K
+    the op cannot take)."""
+    if k % W8A8_GROUP:
+        return None
     if group_size == 0:
+        return w_s.reshape(-1).float().contiguous() if w_s.numel() == n else None
+    if group_size == W8A8_GROUP and tuple(w_s.shape) == (n, k // W8A8_GROUP):
+        return w_s.float().t().contiguous()
+    return None
+
+
+def prepare_w8(w_q: torch.Tensor, w_s: torch.Tensor, group_size: int) -> W8Weights:
+    """Load-time preparation of one W8A16 layer: uint8 rows [N, K] and its
+    scales (group_size -1 or 0 = per channel)."""
+    g = 0 if group_size in (-1, 0) else group_size
+    n, k = w_q.shape
+    if g:
+        if tuple(w_s.shape) != (n, k // g):
+            raise RuntimeError(f"strix W8A16: group scales must be [{n}, {k // g}], got {list(w_s.shape)}")
+        w_s = w_s.contiguous()
+    else:
         if w_s.numel() != n:
-            return None
-    elif group_size != _W8A8_GROUP_SIZE or tuple(w_s.shape) != (n, k // group_size):
-        return None
-    if k % _W8A8_GROUP_SIZE:
-        return None
-    entry = _W8A8_PREP.get(id(w_q))
-    if entry is not None and entry[0]() is w_q:
-        return entry[1]
-    s = w_s.reshape(-1).float().contiguous() if group_size == 0 else w_s.float().t().contiguous()
-    if len(_W8A8_PREP) >= _W8A8_PREP_MAX_ENTRIES:
-        _W8A8_PREP.pop(next(iter(_W8A8_PREP)))
-    _W8A8_PREP[id(w_q)] = (weakref.ref(w_q), s)
-    return s
+            raise RuntimeError(f"strix W8A16: per-channel scales must hold {n} values, got {w_s.numel()}")
+        w_s = w_s.reshape(n).contiguous()
+    return W8Weights(w_q, w_s, w8a8_scale_layout(w_s, n, k, g), g)
 
 
-def _apply_impl(x_2d: torch.Tensor, w_q: torch.Tensor, w_s: torch.Tensor, bias: torch.Tensor | None,
-                group_size: int) -> torch.Tensor:
-    """W8A16 per forward. group_size 0 = per channel, else 32 or 128."""
+def _apply_impl(x_2d: torch.Tensor, w_q: torch.Tensor, w_s: torch.Tensor, w8a8_s: torch.Tensor | None,
+                bias: torch.Tensor | None, group_size: int) -> torch.Tensor:
+    """W8A16 per forward. group_size 0 = per channel, else 32, 64 or 128."""
     m = x_2d.size(0)
     x = x_2d.contiguous()
+    s = w_s if w_s.dtype == x.dtype else w_s.to(x.dtype)
     if m <= MAX_SKINNY_BATCH_SIZE:
-        s = w_s if w_s.dtype == x.dtype else w_s.to(x.dtype)
-        out = S.w8a16_skinny_gemm(w_q, x, s, bias, 0, group_size)
-    else:
-        s = w8a8_scales(w_q, w_s, group_size)
-        if s is None:
-            raise RuntimeError(f"strix W8A16: W8A8 path cannot run N={w_q.size(0)} K={w_q.size(1)} "
-                               f"group_size={group_size}")
-        out = S.w8a8_wmma_gemm(w_q, x, s)
-        out = out if bias is None else out + bias
-    return out
+        return S.w8a16_skinny_gemm(w_q, x, s, bias, 0, group_size)
+    if w8a8_s is None:
+        return S.w8a16_gemm(w_q, x, s, bias, group_size)
+    out = S.w8a8_wmma_gemm(w_q, x, w8a8_s)
+    return out if bias is None else out + bias
 
 
-def _apply_fake(x_2d, w_q, w_s, bias, group_size):
+def _apply_fake(x_2d, w_q, w_s, w8a8_s, bias, group_size):
+    return x_2d.new_empty((x_2d.size(0), w_q.size(0)))
+
+
+def _w4_apply_fake(x_2d, w_q, w_s, bias, group_size):
     return x_2d.new_empty((x_2d.size(0), w_q.size(0)))
 
 
@@ -112,8 +135,8 @@ def can_implement_w8(weight_type: str, zero_points: bool, act_type, group_size: 
         return False, "zero points not supported"
     if act_type not in (torch.float16, torch.bfloat16):
         return False, "needs fp16/bf16 activations"
-    if group_size not in (-1, 32, 128):
-        return False, f"group_size {group_size} not in (-1, 32, 128)"
+    if group_size not in (-1, 32, 64, 128):
+        return False, f"group_size {group_size} not in (-1, 32, 64, 128)"
     if k % 128:
         return False, f"K={k} must be a multiple of 128"
     return True, None
@@ -158,25 +181,25 @@ def register() -> None:
             c = self.config
             w_q_raw = getattr(layer, self.w_q_name)
             w_s_raw = getattr(layer, self.w_s_name)
-            unpacked = unpack_quantized_values_into_int32(w_q_raw.data, c.weight_type, packed_dim=w_q_raw.packed_dim)
-            if getattr(w_q_raw, "output_dim", 0) != 0:
-                unpacked = unpacked.t().contiguous()
-            w_q = pack_w8_rows(unpacked)
+            ints = unpack_quantized_values_into_int32(w_q_raw.data, c.weight_type, packed_dim=w_q_raw.packed_dim)
+            rows = pack_w8_rows(ints if getattr(w_q_raw, "output_dim", 0) == 0 else ints.t())
             if w_s_raw.dim() == 2:
                 permute_param_layout_(w_s_raw, input_dim=1, output_dim=0)
-            w_s = w_s_raw.data.contiguous()
-            self._transform_param(layer, self.w_q_name, lambda _: w_q)
-            self._transform_param(layer, self.w_s_name, lambda _: w_s)
+            prep = prepare_w8(rows, w_s_raw.data, c.group_size)
+            self._transform_param(layer, self.w_q_name, lambda _: prep.w_q)
+            self._transform_param(layer, self.w_s_name, lambda _: prep.w_s)
+            setattr(layer, W8A8_SCALE_ATTR, prep.w8a8_s)
 
         def apply_weights(self, layer: torch.nn.Module, x: torch.Tensor, bias: torch.Tensor | None = None):
             w_q, w_s, _ = self._get_weight_params(layer)
             x_2d = x.reshape(-1, x.shape[-1])
             group_size = 0 if self.config.group_size == -1 else self.config.group_size
-            out = torch.ops.vllm.strix_w8a16_apply(x_2d, w_q, w_s, bias, group_size)
+            out = torch.ops.vllm.strix_w8a16_apply(x_2d, w_q, w_s, getattr(layer, W8A8_SCALE_ATTR), bias,
+                                                   group_size)
             return out.reshape(*x.shape[:-1], w_q.size(0))
 
     direct_register_custom_op(op_name="strix_w4a16_apply", op_func=_w4_apply_impl, mutates_args=[],
-                              fake_impl=_apply_fake)
+                              fake_impl=_w4_apply_fake)
     from vllm.model_executor.kernels.linear.mixed_precision.rdna_hybrid_w4a16 import RDNAHybridW4A16LinearKernel
 
     class StrixW4A16LinearKernel(RDNAHybridW4A16LinearKernel):

@@ -314,17 +314,34 @@ def fp8_bad(hidden_states, w1, w2, s1, s2, block_shape, activation, expert_map, 
     return [name for name, ok in checks.items() if not ok]
 
 
+def zp_layout_ok(w: torch.Tensor, z: torch.Tensor | None, group: int | None) -> bool:
+    """vLLM's int4 MoE zero points: uint8 [E, N/2, K/group], two uint4 per
+    byte along N (even n in the low nibble), for weights uint8 [E, N, K/2]
+    (moe_gemm_w4a16_zp reads exactly this)."""
+    if z is None or not group:
+        return False
+    e, n, k2 = w.shape
+    return (z.dtype == torch.uint8 and z.dim() == 3 and n % 2 == 0 and (2 * k2) % group == 0
+            and tuple(z.shape) == (e, n // 2, 2 * k2 // group) and z.stride(2) == 1)
+
+
 def wna16_bad(hidden_states, w1, w2, s1, s2, group, activation, expert_map, a1q_scale=None, a2_scale=None,
-              has_zp=False, has_bias=False, has_lora=False) -> list[str]:
-    """Names of the failed int4-chain checks (python/strix_vllm/moe.py:360-409)."""
+              has_zp=False, has_bias=False, has_lora=False, z1=None, z2=None) -> list[str]:
+    """Names of the failed int4-chain checks (python/strix_vllm/moe.py:360-409).
+    Unlike the reference (which rejects zero points, python/strix_vllm/moe.py:
+    376), asymmetric experts pass when both zero-point tensors have vLLM's
+    packed layout (`zp_layout_ok`); they then run moe_gemm_w4a16_zp."""
     scale_dtypes = (torch.bfloat16, torch.float16, torch.float32)
+    zp_scale_dtypes = (torch.bfloat16, torch.float16)
     checks = {
         "2d": hidden_states.dim() == 2,
         "act_dtype": hidden_states.dtype == torch.bfloat16,
         "w1_uint8": w1.dtype == torch.uint8,
         "w2_uint8": w2.dtype == torch.uint8,
         "act_scales": a1q_scale is None and a2_scale is None,
-        "zero_point": not has_zp,
+        "zero_point": not has_zp or (zp_layout_ok(w1, z1, group) and zp_layout_ok(w2, z2, group)
+                                     and s1 is not None and s2 is not None
+                                     and s1.dtype in zp_scale_dtypes and s2.dtype in zp_scale_dtypes),
         "group": group in (32, 64, 128),
         "scales": s1 is not None and s2 is not None and s1.dtype in scale_dtypes and s2.dtype in scale_dtypes,
         "bias": not has_bias,
@@ -333,6 +350,32 @@ def wna16_bad(hidden_states, w1, w2, s1, s2, group, activation, expert_map, a1q_
         "activation": _act(activation) in _FUSED,
         "w13_row": w1.size(2) % 8 == 0,
         "w2_row": w2.size(2) % 8 == 0,
+    }
+    return [name for name, ok in checks.items() if not ok]
+
+
+def mxfp4_bad(hidden_states, w1, w2, s1, s2, activation, expert_map, a1q_scale=None, has_bias=False,
+              has_lora=False) -> list[str]:
+    """Names of the failed MXFP4-chain checks ([] = eligible): e2m1 experts
+    uint8 [E, N, K/2] with e8m0 uint8 [E, N, K/32], bf16 activations, a
+    fused gate activation, no biases (the reference has no MXFP4 MoE chain)."""
+    def scales_ok(w, s):
+        return (s is not None and s.dtype == torch.uint8 and s.dim() == 3
+                and tuple(s.shape) == (w.size(0), w.size(1), 2 * w.size(2) // 32) and s.stride(2) == 1)
+
+    checks = {
+        "2d": hidden_states.dim() == 2,
+        "act_dtype": hidden_states.dtype == torch.bfloat16 and a1q_scale is None,
+        "w1_uint8": w1.dtype == torch.uint8 and w1.dim() == 3,
+        "w2_uint8": w2.dtype == torch.uint8 and w2.dim() == 3,
+        "scales": w1.dim() == 3 and w2.dim() == 3 and scales_ok(w1, s1) and scales_ok(w2, s2),
+        "bias": not has_bias,
+        "lora": not has_lora,
+        "expert_map": expert_map is None,
+        "activation": _act(activation) in _FUSED,
+        "k32": w1.dim() == 3 and w2.dim() == 3 and (2 * w1.size(2)) % 64 == 0 and (2 * w2.size(2)) % 64 == 0,
+        "n16": w1.dim() == 3 and w2.dim() == 3 and w1.size(1) % 32 == 0 and w2.size(1) % 16 == 0,
+        "aligned": w1.dim() == 3 and w2.dim() == 3 and w1.stride(1) % 16 == 0 and w2.stride(1) % 16 == 0,
     }
     return [name for name, ok in checks.items() if not ok]
 
@@ -388,10 +431,11 @@ def _make_wna16_experts_cls():
             a = dict(zip(_APPLY_ARGS, args), **kwargs)
             bs = self.block_shape
             group = None if not bs or len(bs) < 2 else int(bs[1])
+            z1, z2 = self.w1_zp, self.w2_zp
+            has_zp = z1 is not None or z2 is not None
             bad = wna16_bad(a["hidden_states"], a["w1"], a["w2"], self.w1_scale, self.w2_scale, group,
-                            a["activation"], a["expert_map"], a["a1q_scale"], a["a2_scale"],
-                            self.w1_zp is not None or self.w2_zp is not None,
-                            self.w1_bias is not None or self.w2_bias is not None, _lora(self))
+                            a["activation"], a["expert_map"], a["a1q_scale"], a["a2_scale"], has_zp,
+                            self.w1_bias is not None or self.w2_bias is not None, _lora(self), z1, z2)
             if bad:
                 from vllm.logger import init_logger
 
@@ -399,10 +443,11 @@ def _make_wna16_experts_cls():
                 return super().apply(**a)
             w1, w2 = a["w1"], a["w2"]
             t = a["hidden_states"].size(0)
-            w4a8 = self._strix_w4a8 and _w4a8_ok(t, group, w1.size(1), w2.size(1))
+            w4a8 = not has_zp and self._strix_w4a8 and _w4a8_ok(t, group, w1.size(1), w2.size(1))
             wna16_experts(a["output"], a["hidden_states"], w1, w2, self.w1_scale, self.w2_scale, a["topk_weights"],
                           a["topk_ids"], group, a["activation"], a["apply_router_weight_on_input"],
-                          a["workspace13"], a["workspace2"], w4a8=w4a8)
+                          a["workspace13"], a["workspace2"], z1=z1 if has_zp else None,
+                          z2=z2 if has_zp else None, w4a8=w4a8)
 
     return StrixTritonWNA16Experts
 
@@ -462,6 +507,54 @@ def _make_int8_experts_cls():
     return StrixInt8Experts
 
 
+def _make_mxfp4_experts_cls():
+    from vllm.model_executor.layers.fused_moe.experts.triton_moe import TritonExperts
+
+    class StrixMxfp4Experts(TritonExperts):
+        """MXFP4 experts (e2m1 + e8m0 per 32 K) on moe_gemm_mxfp4: weights
+        decoded to bf16 in LDS or registers, bf16 MFMA, bf16 activations."""
+
+        @property
+        def expects_unquantized_inputs(self) -> bool:
+            return True
+
+        def apply(self, *args, **kwargs):
+            a = dict(zip(_APPLY_ARGS, args), **kwargs)
+            bad = mxfp4_bad(a["hidden_states"], a["w1"], a["w2"], self.w1_scale, self.w2_scale, a["activation"],
+                            a["expert_map"], a["a1q_scale"],
+                            self.w1_bias is not None or self.w2_bias is not None, _lora(self))
+            if bad:
+                from vllm.logger import init_logger
+
+                init_logger("vllm.strix").warning_once("moe_mxfp4 falls back: " + ", ".join(bad))
+                return super().apply(**a)
+            mxfp4_experts(a["output"], a["hidden_states"], a["w1"], a["w2"], self.w1_scale, self.w2_scale,
+                          a["topk_weights"], a["topk_ids"], a["activation"], a["apply_router_weight_on_input"],
+                          a["workspace13"], a["workspace2"])
+
+    return StrixMxfp4Experts
+
+
+def _hook_backend(oracle_mod, enum_name: str, cls) -> bool:
+    """Route an oracle module's Triton backend to `cls` (the FP8 / int8 /
+    MXFP4 oracles of vLLM pick experts classes through
+    `backend_to_kernel_cls(backend)`). False when the module has no such
+    selector or enum member (another vLLM version): the hook is skipped."""
+    enum = getattr(oracle_mod, enum_name, None)
+    orig = getattr(oracle_mod, "backend_to_kernel_cls", None)
+    triton = getattr(enum, "TRITON", None) if enum is not None else None
+    if orig is None or triton is None:
+        return False
+
+    def _backend_to_kernel_cls(backend, _orig=orig, _cls=cls, _triton=triton):
+        if backend == _triton:
+            return [_cls]
+        return _orig(backend)
+
+    oracle_mod.backend_to_kernel_cls = _backend_to_kernel_cls
+    return True
+
+
 def register() -> None:
     """Hook vLLM's MoE selection (python/strix_vllm/moe.py:1019-1108): the
     unquantized method's experts class, the WNA16 oracle's module global and
@@ -489,25 +582,19 @@ def register() -> None:
     if not disabled("moe_fp8"):
         from vllm.model_executor.layers.fused_moe.oracle import fp8 as fp8_oracle
 
-        fp8_cls = _make_fp8_experts_cls(w8a8=not disabled("moe_fp8_w8a8"))
-        fp8_orig = fp8_oracle.backend_to_kernel_cls
-
-        def _fp8_backend_to_kernel_cls(backend, _orig=fp8_orig, _cls=fp8_cls):
-            if backend == fp8_oracle.Fp8MoeBackend.TRITON:
-                return [_cls]
-            return _orig(backend)
-
-        fp8_oracle.backend_to_kernel_cls = _fp8_backend_to_kernel_cls
+        _hook_backend(fp8_oracle, "Fp8MoeBackend", _make_fp8_experts_cls(w8a8=not disabled("moe_fp8_w8a8")))
 
     if os.environ.get("STRIX_MOE_W8A16") and not disabled("moe_w8a16"):
         from vllm.model_executor.layers.fused_moe.oracle import int8 as int8_oracle
 
-        cls8 = _make_int8_experts_cls()
-        orig8 = int8_oracle.backend_to_kernel_cls
+        _hook_backend(int8_oracle, "Int8MoeBackend", _make_int8_experts_cls())
 
-        def _int8_backend_to_kernel_cls(backend, _orig=orig8, _cls=cls8):
-            if backend == int8_oracle.Int8MoeBackend.TRITON:
-                return [_cls]
-            return _orig(backend)
+    if not disabled("moe_mxfp4"):
+        try:
+            from vllm.model_executor.layers.fused_moe.oracle import mxfp4 as mxfp4_oracle
+        except ImportError:
+            mxfp4_oracle = None
+        if mxfp4_oracle is None or not _hook_backend(mxfp4_oracle, "Mxfp4MoeBackend", _make_mxfp4_experts_cls()):
+            from vllm.logger import init_logger
 
-        int8_oracle.backend_to_kernel_cls = _int8_backend_to_kernel_cls
+            init_logger("vllm.strix").info("moe_mxfp4: this vLLM has no MXFP4 MoE backend selector; not hooked")

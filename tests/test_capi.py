@@ -45,6 +45,13 @@ def test_every_declared_symbol_is_exported_and_bound():
         ("strix_moe_align", (0, 16, 4, 16, 0, 10, 0, 10, 0, 0, 0, 0), "sorted_ids needs"),
         ("strix_moe_sum", (0, 0, 100, 1, 8, 100, 0, 0, 100, 0), "multiples of 8"),
         ("strix_probe_mfma", (1, 0, 0, 0, 100, 0), "multiple of 128"),
+        # Operands whose rows span more than 4 GiB overflow the kernels' 32-bit row offsets.
+        ("strix_fp8_w8a8_block_gemm", (0, 5120, 0, 40, 0, 5120, 0, 40, 0, 128, 0, 900000, 128, 5120, -1, 0),
+         "more than 4 GiB"),
+        ("strix_w8a8_int8_gemm", (0, 5120, 0, 0, 5120, 0, 0, 128, 0, 900000, 128, 5120, -1, 0),
+         "more than 4 GiB"),
+        ("strix_w16_gemm", (1, 0, 2560, 0, 3, 160, 1, 32, 1, 0, 0, 5120, 0, 0, 0, 128, 0, 450000, 128, 5120, -1,
+                            0), "more than 4 GiB"),
     ],
 )
 def test_argument_errors_without_gpu(fn, args, msg):

@@ -189,12 +189,13 @@ def test_config3_fused_moe(t, c3_weights):
     out = functional.fused_moe_fp8_w8a8(x.to(DEV), logits.to(DEV), dev["w13"], dev["w13_s"], dev["w2"],
                                         dev["w2_s"], 8)
     ids, w = oracle.route_topk(logits, 8)
-    rows = list(range(t)) if t <= 64 else torch.randperm(t, generator=g)[:32].tolist()
+    # Every token row is checked (the output starts uninitialized, so a row
+    # the chain never writes fails).
     ref = oracle.fused_moe(x, ids, w,
                            lambda e: oracle.fp8_block_dequant(d["w13"][e], d["w13_s"][e]),
-                           lambda e: oracle.fp8_block_dequant(d["w2"][e], d["w2_s"][e]),
-                           act_quant="fp8", tokens=rows)
-    assert peak_rel_err(out.cpu()[rows], ref) <= TOL
+                           lambda e: oracle.fp8_block_dequant(d["w2"][e], d["w2_s"][e]), act_quant="fp8")
+    assert ref.shape == out.shape
+    assert peak_rel_err(out, ref) <= TOL
 
 
 @pytest.mark.parametrize("t", [1, 64, 700])

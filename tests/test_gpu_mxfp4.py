@@ -180,7 +180,8 @@ def test_config4_fused_moe(t, c4_weights):
     logits = torch.randn(t, 32, generator=g)
     out = functional.fused_moe_mxfp4(x.to(DEV), logits.to(DEV), dev["w13"], dev["w13_s"], dev["w2"], dev["w2_s"], 4)
     ids, w = oracle.route_topk(logits, 4)
-    rows = list(range(t)) if t <= 64 else torch.randperm(t, generator=g)[:24].tolist()
+    # Every token row is checked.
     ref = oracle.fused_moe(x, ids, w, lambda e: oracle.mxfp4_decode(d["w13"][e], d["w13_s"][e]),
-                           lambda e: oracle.mxfp4_decode(d["w2"][e], d["w2_s"][e]), tokens=rows)
-    assert peak_rel_err(out.cpu()[rows], ref) <= TOL
+                           lambda e: oracle.mxfp4_decode(d["w2"][e], d["w2_s"][e]))
+    assert ref.shape == out.shape
+    assert peak_rel_err(out, ref) <= TOL

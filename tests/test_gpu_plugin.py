@@ -77,6 +77,20 @@ def test_fp8_linear_w8a16(m, scales):
     assert peak_rel_err(out, x.float() @ wf.t() + bias.float()) <= TOL
 
 
+@pytest.mark.parametrize("m", [1, 200])
+def test_fp8_channel_square_weight_through_load_transform(m):
+    # A square weight handed over as vLLM's [K, N] view: the load transform
+    # must restore [N, K] rows from the strides (sizes cannot tell N from K).
+    n = k = 1024
+    w, _ = _fp8_weights(n, k, 31 + m)
+    s = torch.rand(n, generator=_g(m)) * 0.02 + 0.005
+    wc, sc = fp8.prepare_channel(w.to(DEV).t(), s.to(DEV), n)
+    x = torch.randn(m, k, generator=_g(m + 5)).to(torch.bfloat16)
+    out = fp8._apply_impl(x.to(DEV), wc, sc, None, False).cpu()
+    wf = oracle.e4m3_decode(w.view(torch.uint8)) * s[:, None]
+    assert peak_rel_err(out, x.float() @ wf.t()) <= TOL
+
+
 @pytest.mark.parametrize("m,bias", [(1, False), (5, False), (3, True), (64, False), (mxfp4.DEQUANT_MIN_M, True),
                                     (300, False)])
 def test_mxfp4_linear(m, bias):
@@ -93,7 +107,7 @@ def test_mxfp4_linear(m, bias):
 
 
 @pytest.mark.parametrize("m", [1, 8, 9, 200])
-@pytest.mark.parametrize("group", [0, 128])
+@pytest.mark.parametrize("group", [0, 32, 64, 128])
 def test_w8a16_linear(m, group):
     n, k = 512, 1024
     g = _g(m + group)
@@ -102,10 +116,10 @@ def test_w8a16_linear(m, group):
     if group == 0:
         s = s.reshape(n)
     x = torch.randn(m, k, generator=g).to(torch.bfloat16)
-    linear._W8A8_PREP.clear()
-    out = linear._apply_impl(x.to(DEV), w.to(DEV), s.to(DEV), None, group).cpu()
+    p = linear.prepare_w8(w.to(DEV), s.to(DEV), group)
+    out = linear._apply_impl(x.to(DEV), p.w_q, p.w_s, p.w8a8_s, None, group).cpu()
     wf = oracle.u8b128_decode(w, s, group)
-    if m <= linear.MAX_SKINNY_BATCH_SIZE:
+    if m <= linear.MAX_SKINNY_BATCH_SIZE or p.w8a8_s is None:   # bf16 activations as given
         ref = x.float() @ wf.t()
     else:   # the W8A8 op quantizes the activations per (row, 128) inside
         qa, sa = oracle.int8_quant_group128(x)
@@ -217,6 +231,60 @@ def test_wna16_experts_symmetric(t, group):
                             ids.to(DEV), group).cpu()
     ref = oracle.fused_moe(x, ids, tw, oracle.wna16_sym_decode(w13, s13, group),
                            oracle.wna16_sym_decode(w2, s2, group))
+    assert peak_rel_err(out, ref) <= TOL
+
+
+@pytest.mark.parametrize("t", [2, 300])
+@pytest.mark.parametrize("group", [64, 128])
+def test_wna16_experts_zero_points(t, group):
+    # The vLLM WNA16 class passes w1_zp / w2_zp (uint8 [E, N/2, K/G], even n
+    # in the low nibble) with uint8 [E, N, K/2] weights: (q - z) * s.
+    e, top_k, h, inter = 8, 2, 512, 256
+    g = _g(190 + t + group)
+    q13 = torch.randint(0, 16, (e, 2 * inter, h), generator=g, dtype=torch.uint8)
+    q2 = torch.randint(0, 16, (e, h, inter), generator=g, dtype=torch.uint8)
+    pack = lambda q: (q[..., 0::2] | (q[..., 1::2] << 4)).contiguous()
+    zpack = lambda z: (z[..., 0::2, :] | (z[..., 1::2, :] << 4)).contiguous()
+    z13 = torch.randint(0, 16, (e, 2 * inter, h // group), generator=g, dtype=torch.uint8)
+    z2 = torch.randint(0, 16, (e, h, inter // group), generator=g, dtype=torch.uint8)
+    s13 = (torch.rand(e, 2 * inter, h // group, generator=g) * 0.02 + 0.002).to(torch.bfloat16)
+    s2 = (torch.rand(e, h, inter // group, generator=g) * 0.02 + 0.002).to(torch.bfloat16)
+    x = torch.randn(t, h, generator=g).to(torch.bfloat16)
+    ids, tw = _route(t, e, top_k, t + 6)
+    w13, w2, zz13, zz2 = pack(q13), pack(q2), zpack(z13), zpack(z2)
+    out = moe.wna16_experts(None, x.to(DEV), w13.to(DEV), w2.to(DEV), s13.to(DEV), s2.to(DEV), tw.to(DEV),
+                            ids.to(DEV), group, z1=zz13.to(DEV), z2=zz2.to(DEV)).cpu()
+    ref13 = (q13.float() - z13.repeat_interleave(group, -1).float()) * s13.float().repeat_interleave(group, -1)
+    ref2 = (q2.float() - z2.repeat_interleave(group, -1).float()) * s2.float().repeat_interleave(group, -1)
+    # The oracle's decode of the same bytes (uint8 [E, N, K/2] viewed as int32 words) agrees.
+    assert torch.equal(oracle.wna16_zp_decode(w13.view(torch.int32), s13, zz13, group), ref13)
+    ref = oracle.fused_moe(x, ids, tw, ref13, ref2)
+    assert peak_rel_err(out, ref) <= TOL
+
+
+def test_awq_checkpoint_through_zero_point_experts():
+    # AWQ-layout experts ([E, K, N/8] words in AutoAWQ's nibble order), converted
+    # on the device at load, then the zero-point expert chain.
+    from libstrix_amd import convert
+    from test_convert import awq_pack_reference
+
+    e, top_k, h, inter, group, t = 4, 2, 256, 128, 128, 37
+    g = _g(777)
+    q13 = torch.randint(0, 16, (e, h, 2 * inter), generator=g)     # AWQ is [K, N]
+    q2 = torch.randint(0, 16, (e, inter, h), generator=g)
+    z13 = torch.randint(0, 16, (e, h // group, 2 * inter), generator=g)
+    z2 = torch.randint(0, 16, (e, inter // group, h), generator=g)
+    s13 = torch.rand(e, h // group, 2 * inter, generator=g).to(torch.float16) * 0.02 + 0.002
+    s2 = torch.rand(e, inter // group, h, generator=g).to(torch.float16) * 0.02 + 0.002
+    pk = lambda v: torch.stack([awq_pack_reference(v[i]) for i in range(e)])
+    b13, c13, y13 = convert.awq_to_wna16(pk(q13).to(DEV), pk(z13).to(DEV), s13.to(DEV))
+    b2, c2, y2 = convert.awq_to_wna16(pk(q2).to(DEV), pk(z2).to(DEV), s2.to(DEV))
+    x = torch.randn(t, h, generator=g).to(torch.bfloat16)
+    ids, tw = _route(t, e, top_k, 9)
+    out = moe.wna16_experts(None, x.to(DEV), b13, b2, c13, c2, tw.to(DEV), ids.to(DEV), group, z1=y13, z2=y2).cpu()
+    deq = lambda q, z, sc: ((q.float() - z.float().repeat_interleave(group, 1))
+                            * sc.to(torch.bfloat16).float().repeat_interleave(group, 1)).transpose(1, 2)
+    ref = oracle.fused_moe(x, ids, tw, deq(q13, z13, s13), deq(q2, z2, s2))
     assert peak_rel_err(out, ref) <= TOL
 
 

@@ -105,8 +105,9 @@ def test_config5_fused_moe(t, c5_weights):
     out = functional.fused_moe_wna16(x.to(DEV), logits.to(DEV), dev["w13"], dev["w13_s"], dev["w13_z"], dev["w2"],
                                      dev["w2_s"], dev["w2_z"], 8, 128)
     ids, w = oracle.route_topk(logits, 8)
-    rows = list(range(t)) if t <= 64 else torch.randperm(t, generator=g)[:24].tolist()
+    # Every token row is checked.
     ref = oracle.fused_moe(x, ids, w,
                            lambda e: oracle.wna16_zp_decode(d["w13"][e], d["w13_s"][e], d["w13_z"][e], 128),
-                           lambda e: oracle.wna16_zp_decode(d["w2"][e], d["w2_s"][e], d["w2_z"][e], 128), tokens=rows)
-    assert peak_rel_err(out.cpu()[rows], ref) <= TOL
+                           lambda e: oracle.wna16_zp_decode(d["w2"][e], d["w2_s"][e], d["w2_z"][e], 128))
+    assert ref.shape == out.shape
+    assert peak_rel_err(out, ref) <= TOL

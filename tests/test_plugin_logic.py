@@ -50,6 +50,7 @@ _OUT = {
     "mxfp4_wmma_gemm": lambda w, x, s, b: torch.zeros(x.size(0), w.size(0), dtype=torch.bfloat16),
     "w8a16_skinny_gemm": lambda w, x, s, b, cu, g: torch.zeros(x.size(0), w.size(0), dtype=x.dtype),
     "w8a8_wmma_gemm": lambda w, x, s: torch.zeros(x.size(0), w.size(0), dtype=x.dtype),
+    "w8a16_gemm": lambda w, x, s, b, g: torch.zeros(x.size(0), w.size(0), dtype=x.dtype),
     "w4a16_dequant": lambda w, s, g: torch.zeros(w.size(0), 2 * w.size(1), dtype=torch.bfloat16),
     "w4a16_wmma_gemm": lambda x, w, s, b, g: torch.zeros(x.size(0), w.size(0), dtype=torch.bfloat16),
     "moe_align": lambda ids, e, bm: (torch.zeros(64, dtype=torch.int32), torch.zeros(4, dtype=torch.int32),
@@ -100,7 +101,16 @@ def test_cache_factor_tracks_activity_and_env(clean_env):
     a, b = plugin._cache_factor(True), plugin._cache_factor(False)
     assert len(a) == 16 and a != b and a == plugin._cache_factor(True)
     clean_env.setenv("STRIX_DISABLE", "fp8")
-    assert plugin._cache_factor(True) != a
+    d = plugin._cache_factor(True)
+    assert d != a
+    clean_env.setenv("STRIX_DISABLE", " fp8 ,")                 # the same set of names: the same key
+    assert plugin._cache_factor(True) == d
+    clean_env.setenv("STRIX_DISABLE", "fp8,mxfp4")
+    assert plugin._cache_factor(True) != d
+
+
+def test_model_architectures_without_vllm():
+    assert plugin._model_architectures() == []
 
 
 def test_not_on_gfx950_without_a_gpu():
@@ -181,6 +191,14 @@ def test_wna16_moe_eligibility():
     assert moe.wna16_bad(x, w1, w2, s1, s2, 128, "silu", None) == []
     assert moe.wna16_bad(x, w1, w2, s1, s2, 16, "silu", None) == ["group"]
     assert moe.wna16_bad(x, w1, w2, s1, s2, 128, "silu", None, has_zp=True) == ["zero_point"]
+    z1 = torch.zeros(e, n // 2, k // 128, dtype=torch.uint8)      # vLLM's packed zero points: eligible
+    z2 = torch.zeros(e, k // 2, (n // 2) // 128, dtype=torch.uint8)
+    assert moe.wna16_bad(x, w1, w2, s1, s2, 128, "silu", None, has_zp=True, z1=z1, z2=z2) == []
+    assert moe.wna16_bad(x, w1, w2, s1, s2, 128, "silu", None, has_zp=True, z1=z1, z2=None) == ["zero_point"]
+    assert moe.wna16_bad(x, w1, w2, s1.float(), s2, 128, "silu", None, has_zp=True, z1=z1,
+                         z2=z2) == ["zero_point"]                 # the zp kernel takes bf16/fp16 scales
+    assert moe.wna16_bad(x, w1, w2, s1, s2, 128, "silu", None, has_zp=True,
+                         z1=torch.zeros(e, n, k // 128, dtype=torch.uint8), z2=z2) == ["zero_point"]
     assert moe.wna16_bad(x.half(), w1, w2, s1, s2, 128, "silu", None) == ["act_dtype"]
 
 
@@ -232,22 +250,44 @@ def test_mxfp4_weight_checks():
     assert not mxfp4.can_implement(True, torch.float16)[0]
 
 
-def test_w8a8_scales_layout_and_cache():
-    linear._W8A8_PREP.clear()
+def test_w8_prepare_scale_layouts():
     w = torch.zeros(64, 256, dtype=torch.uint8)
     s = torch.rand(64, 2, dtype=torch.bfloat16)
-    g = linear.w8a8_scales(w, s, 128)
-    assert g.shape == (2, 64) and torch.equal(g, s.float().t())
-    assert linear.w8a8_scales(w, s, 128) is g                  # cached per weight
-    linear._W8A8_PREP.clear()
-    assert linear.w8a8_scales(w, torch.rand(64, 1), 0).shape == (64,)
-    assert linear.w8a8_scales(torch.zeros(64, 256, dtype=torch.uint8), torch.rand(64, 8), 32) is None
+    p = linear.prepare_w8(w, s, 128)
+    assert p.group_size == 128 and p.w8a8_s.shape == (2, 64) and torch.equal(p.w8a8_s, s.float().t())
+    assert p.w8a8_s.dtype == torch.float32 and p.w8a8_s.is_contiguous()
+    pc = linear.prepare_w8(w, torch.rand(64, 1), -1)           # per channel: [N] for both paths
+    assert pc.group_size == 0 and pc.w_s.shape == (64,) and pc.w8a8_s.shape == (64,)
+    for g in (32, 64):                                           # no W8A8 layout: W8A16 at every M
+        pg = linear.prepare_w8(w, torch.rand(64, 256 // g), g)
+        assert pg.w8a8_s is None and pg.w_s.shape == (64, 256 // g)
+    assert linear.prepare_w8(torch.zeros(64, 192, dtype=torch.uint8), torch.rand(64, 1), 0).w8a8_s is None
+    with pytest.raises(RuntimeError, match="group scales"):
+        linear.prepare_w8(w, torch.rand(64, 3), 128)
+    with pytest.raises(RuntimeError, match="per-channel"):
+        linear.prepare_w8(w, torch.rand(32), 0)
     assert torch.equal(linear.pack_w8_rows(torch.tensor([[0, 255, 256 + 7]])), torch.tensor([[0, 255, 7]],
                                                                                              dtype=torch.uint8))
     assert linear.can_implement_w8("uint8b128", False, torch.bfloat16, 128, 5120) == (True, None)
+    assert linear.can_implement_w8("uint8b128", False, torch.bfloat16, 64, 5120) == (True, None)
+    assert not linear.can_implement_w8("uint8b128", False, torch.bfloat16, 16, 5120)[0]
     assert not linear.can_implement_w8("uint4b8", False, torch.bfloat16, 128, 5120)[0]
     assert linear.can_implement_w4("uint4b8", False, 64, 5120) == (True, None)
     assert not linear.can_implement_w4("uint4b8", True, 64, 5120)[0]
+
+
+def test_fp8_channel_prepare_square_weight():
+    # A square [K, N] view (vLLM's per-channel layout) must be transposed back
+    # to [N, K] rows even though its sizes cannot tell the orientation.
+    w = torch.arange(256 * 256, dtype=torch.float32).reshape(256, 256).remainder(97).to(torch.float8_e4m3fn)
+    wc, _ = fp8.prepare_channel(w.t(), torch.ones(256), 256)
+    assert torch.equal(wc.view(torch.uint8), w.view(torch.uint8)) and wc.is_contiguous()
+    wr, _ = fp8.prepare_channel(w, torch.ones(256), 256)       # row-major [N, K] stays as is
+    assert torch.equal(wr.view(torch.uint8), w.view(torch.uint8))
+    wk, _ = fp8.prepare_channel(w[:, :128].contiguous(), torch.ones(128), 128)   # stored [K, N]: transposed
+    assert wk.shape == (128, 256)
+    with pytest.raises(RuntimeError, match="no dimension"):
+        fp8.prepare_channel(w[:100, :200], torch.ones(64), 64)
 
 
 # ------------------------------------------------------------------ per-forward dispatch
@@ -293,16 +333,20 @@ def test_mxfp4_dispatch(rec, m, bias, expect):
 
 @pytest.mark.parametrize("m,expect", [(1, "w8a16_skinny_gemm"), (8, "w8a16_skinny_gemm"), (9, "w8a8_wmma_gemm")])
 def test_w8a16_dispatch(rec, m, expect):
-    linear._W8A8_PREP.clear()
-    linear._apply_impl(torch.zeros(m, 256, dtype=torch.bfloat16), torch.zeros(64, 256, dtype=torch.uint8),
-                       torch.ones(64, 2, dtype=torch.bfloat16), None, 128)
+    p = linear.prepare_w8(torch.zeros(64, 256, dtype=torch.uint8), torch.ones(64, 2, dtype=torch.bfloat16), 128)
+    linear._apply_impl(torch.zeros(m, 256, dtype=torch.bfloat16), p.w_q, p.w_s, p.w8a8_s, None, p.group_size)
     assert rec.calls == [expect]
+    if expect == "w8a8_wmma_gemm":
+        assert rec.args[0][2] is p.w8a8_s                          # the load-time scales, no per-call copy
 
 
-def test_w8a16_group32_prefill_raises(rec):
-    with pytest.raises(RuntimeError, match="cannot run"):
-        linear._apply_impl(torch.zeros(20, 256, dtype=torch.bfloat16), torch.zeros(64, 256, dtype=torch.uint8),
-                           torch.ones(64, 8, dtype=torch.bfloat16), None, 32)
+@pytest.mark.parametrize("group", [32, 64])
+@pytest.mark.parametrize("m,expect", [(8, "w8a16_skinny_gemm"), (20, "w8a16_gemm"), (4096, "w8a16_gemm")])
+def test_w8a16_small_group_prefill_stays_w8a16(rec, group, m, expect):
+    p = linear.prepare_w8(torch.zeros(64, 256, dtype=torch.uint8), torch.ones(64, 256 // group,
+                                                                              dtype=torch.bfloat16), group)
+    out = linear._apply_impl(torch.zeros(m, 256, dtype=torch.bfloat16), p.w_q, p.w_s, p.w8a8_s, None, group)
+    assert rec.calls == [expect] and out.shape == (m, 64)
 
 
 @pytest.mark.parametrize("m,expect", [(1, "w4a16_wmma_gemm"), (mxfp4.DEQUANT_MIN_M - 1, "w4a16_wmma_gemm"),
@@ -389,3 +433,110 @@ def test_mxfp4_and_int8_chains(rec):
                      dtype=torch.int8), torch.ones(e, 2 * inter), torch.ones(e, h), w, ids)
     assert rec.calls == ["moe_align", "moe_gemm_mxfp4", "moe_gemm_mxfp4", "moe_sum",
                          "moe_align", "moe_gemm_w8a16", "moe_gemm_w8a16", "moe_sum"]
+
+
+# ------------------------------------------------------------------ vLLM hook classes (stub vLLM)
+class _StubExperts:
+    """Stands in for vLLM's TritonExperts / TritonWNA16Experts: `apply` is the
+    fallback the Strix classes call when a layer is not eligible."""
+
+    fell: list = []
+
+    def __init__(self, *args, **kwargs):
+        self.block_shape = None
+        self.w1_scale = self.w2_scale = None
+        self.w1_zp = self.w2_zp = None
+        self.w1_bias = self.w2_bias = None
+
+    def apply(self, **kwargs):
+        self.fell.append(kwargs)   # the class-level list of the stub base, shared by subclasses
+
+
+class _StubLogger:
+    def warning_once(self, *a):
+        pass
+
+    info = warning_once
+
+
+@pytest.fixture
+def stub_vllm(monkeypatch):
+    import sys
+    import types
+
+    names = ["vllm", "vllm.model_executor", "vllm.model_executor.layers", "vllm.model_executor.layers.fused_moe",
+             "vllm.model_executor.layers.fused_moe.experts", "vllm.model_executor.layers.fused_moe.experts.triton_moe",
+             "vllm.logger"]
+    mods = {n: types.ModuleType(n) for n in names}
+    tm = mods["vllm.model_executor.layers.fused_moe.experts.triton_moe"]
+    tm.TritonExperts = type("TritonExperts", (_StubExperts,), {"fell": []})
+    tm.TritonWNA16Experts = type("TritonWNA16Experts", (_StubExperts,), {"fell": []})
+    mods["vllm.logger"].init_logger = lambda name: _StubLogger()
+    for n, m in mods.items():
+        monkeypatch.setitem(sys.modules, n, m)
+    return tm
+
+
+def _apply_kwargs(x, w1, w2, ids, tw):
+    return dict(output=None, hidden_states=x, w1=w1, w2=w2, topk_weights=tw, topk_ids=ids, activation="silu",
+                global_num_experts=w1.size(0), expert_map=None, a1q_scale=None, a2_scale=None, workspace13=None,
+                workspace2=None, expert_tokens_meta=None, apply_router_weight_on_input=False)
+
+
+def test_wna16_class_runs_zero_points(rec, stub_vllm, clean_env):
+    e, n, k, t, top_k = 4, 256, 512, 3, 2
+    cls = moe._make_wna16_experts_cls()
+    ex = cls()
+    ex.block_shape = [0, 128]
+    ex.w1_scale = torch.ones(e, n, k // 128, dtype=torch.bfloat16)
+    ex.w2_scale = torch.ones(e, k, (n // 2) // 128, dtype=torch.bfloat16)
+    ex.w1_zp = torch.zeros(e, n // 2, k // 128, dtype=torch.uint8)
+    ex.w2_zp = torch.zeros(e, k // 2, (n // 2) // 128, dtype=torch.uint8)
+    x = torch.zeros(t, k, dtype=torch.bfloat16)
+    w1 = torch.zeros(e, n, k // 2, dtype=torch.uint8)
+    w2 = torch.zeros(e, k, n // 4, dtype=torch.uint8)
+    ids, tw = torch.zeros(t, top_k, dtype=torch.int32), torch.rand(t, top_k)
+    ex.apply(**_apply_kwargs(x, w1, w2, ids, tw))
+    assert rec.calls == ["moe_align", "moe_gemm_w4a16_zp", "moe_gemm_w4a16_zp", "moe_sum"]
+    assert rec.args[1][4] is ex.w1_zp and rec.args[2][4] is ex.w2_zp
+    assert not stub_vllm.TritonWNA16Experts.fell
+    # Zero points in another layout (one byte per n): vLLM's own kernel runs.
+    ex.w1_zp = torch.zeros(e, n, k // 128, dtype=torch.uint8)
+    ex.apply(**_apply_kwargs(x, w1, w2, ids, tw))
+    assert len(stub_vllm.TritonWNA16Experts.fell) == 1 and len(rec.calls) == 4
+
+
+def test_mxfp4_class_and_gate(rec, stub_vllm, clean_env):
+    e, n, k, t, top_k = 4, 256, 512, 5, 2
+    ex = moe._make_mxfp4_experts_cls()()
+    assert ex.expects_unquantized_inputs
+    ex.w1_scale = torch.zeros(e, n, k // 32, dtype=torch.uint8)
+    ex.w2_scale = torch.zeros(e, k, (n // 2) // 32, dtype=torch.uint8)
+    x = torch.zeros(t, k, dtype=torch.bfloat16)
+    w1 = torch.zeros(e, n, k // 2, dtype=torch.uint8)
+    w2 = torch.zeros(e, k, n // 4, dtype=torch.uint8)
+    ids, tw = torch.zeros(t, top_k, dtype=torch.int32), torch.rand(t, top_k)
+    ex.apply(**_apply_kwargs(x, w1, w2, ids, tw))
+    assert rec.calls == ["moe_align", "moe_gemm_mxfp4", "moe_gemm_mxfp4", "moe_sum"]
+    ex.w1_bias = torch.zeros(e, n)                                  # biases (e.g. gpt-oss): vLLM's own path
+    ex.apply(**_apply_kwargs(x, w1, w2, ids, tw))
+    assert len(stub_vllm.TritonExperts.fell) == 1 and len(rec.calls) == 4
+    assert moe.mxfp4_bad(x, w1, w2, ex.w1_scale, ex.w2_scale, "silu", None) == []
+    assert moe.mxfp4_bad(x, w1, w2, ex.w1_scale.float(), ex.w2_scale, "silu", None) == ["scales"]
+    assert moe.mxfp4_bad(x, w1, w2, ex.w1_scale, ex.w2_scale, "swigluoai", None) == ["activation"]
+    assert moe.mxfp4_bad(x.half(), w1, w2, ex.w1_scale, ex.w2_scale, "silu", None) == ["act_dtype"]
+
+
+def test_backend_hook_routes_triton_only():
+    import enum
+    import types
+
+    class Backend(enum.Enum):
+        TRITON = 1
+        OTHER = 2
+
+    mod = types.SimpleNamespace(Mxfp4MoeBackend=Backend, backend_to_kernel_cls=lambda b: ["vllm-own"])
+    assert moe._hook_backend(mod, "Mxfp4MoeBackend", "strix-cls")
+    assert mod.backend_to_kernel_cls(Backend.TRITON) == ["strix-cls"]
+    assert mod.backend_to_kernel_cls(Backend.OTHER) == ["vllm-own"]
+    assert not moe._hook_backend(types.SimpleNamespace(), "Mxfp4MoeBackend", "strix-cls")
