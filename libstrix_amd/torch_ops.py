@@ -65,6 +65,11 @@ def _check(cond: bool, msg: str) -> None:
         raise RuntimeError(msg)
 
 
+def _unit_last(t: torch.Tensor) -> bool:
+    """The last dim is unit-stride, or has one element (then its stride is never used)."""
+    return t.size(-1) == 1 or t.stride(-1) == 1
+
+
 def _rowmajor(t: torch.Tensor, what: str) -> None:
     _check(t.dim() == 2 and t.stride(1) == 1, f"{what} must be 2-D and contiguous in dim 1")
 
@@ -355,7 +360,7 @@ def moe_gemm_fp8_w8a8(c, qa, sa, b, scales, sorted_ids, expert_ids, num_post_pad
     _check(sa.dtype == torch.float32 and sa.dim() == 2 and sa.size(1) == k // 128 and sa.stride(1) == 1,
            "sa must be float32 [rows, K/128]")
     _check(scales.dtype == torch.float32 and tuple(scales.shape) == (e, (n + 127) // 128, k // 128)
-           and scales.stride(2) == 1, "scales must be float32 [E, N/128, K/128]")
+           and _unit_last(scales), "scales must be float32 [E, N/128, K/128]")
     _check(c.dim() == 2 and c.stride(1) == 1 and c.dtype in (torch.bfloat16, torch.float16), "c must be bf16/fp16 2-D")
     _check(n % block_n == 0, f"N={n} is not a multiple of block_n={block_n}")
     _moe_common(c, sorted_ids, expert_ids, num_post_padded, topk_weights, block_m)
@@ -629,7 +634,7 @@ def moe_gemm_mxfp4(c, a, b, scales, sorted_ids, expert_ids, num_post_padded, top
     _check(scales.dtype == torch.uint8, "scale must be uint8 (e8m0)")
     e, n, k2 = b.shape
     k = 2 * k2
-    _check(tuple(scales.shape) == (e, n, k // 32) and scales.stride(2) == 1, "scales must be e8m0 [E, N, K/32]")
+    _check(tuple(scales.shape) == (e, n, k // 32) and _unit_last(scales), "scales must be e8m0 [E, N, K/32]")
     tail = _moe16_tail(c, a, sorted_ids, expert_ids, num_post_padded, topk_weights, top_k, block_m, silu_mul,
                        activation, n, k)
     _lib.call("strix_moe_gemm_mxfp4", _ptr(b), b.stride(0), b.stride(1), _ptr(scales), scales.stride(0),
@@ -662,8 +667,8 @@ def moe_gemm_w4a16_zp(c, a, b, scales, zeros, sorted_ids, expert_ids, num_post_p
     e, n, k2 = bu.shape
     k = 2 * k2
     _check(scales.dtype in (torch.bfloat16, torch.float16) and tuple(scales.shape) == (e, n, k // group_size)
-           and scales.stride(2) == 1, "scales must be bf16/fp16 [E, N, K/group_size]")
-    _check(zeros.dtype == torch.uint8 and tuple(zeros.shape) == (e, n // 2, k // group_size) and zeros.stride(2) == 1,
+           and _unit_last(scales), "scales must be bf16/fp16 [E, N, K/group_size]")
+    _check(zeros.dtype == torch.uint8 and tuple(zeros.shape) == (e, n // 2, k // group_size) and _unit_last(zeros),
            "zeros must be uint8 [E, N/2, K/group_size] (two uint4 zero points per byte along N)")
     tail = _moe16_tail(c, a, sorted_ids, expert_ids, num_post_padded, topk_weights, top_k, block_m, silu_mul,
                        activation, n, k)
@@ -691,7 +696,7 @@ def moe_gemm_w4a16(c, a, b, scales, sorted_ids, expert_ids, num_post_padded, top
     e, n, k2 = bu.shape
     k = 2 * k2
     _check(scales.dtype in (torch.bfloat16, torch.float16, torch.float32)
-           and tuple(scales.shape) == (e, n, k // group_size) and scales.stride(2) == 1,
+           and tuple(scales.shape) == (e, n, k // group_size) and _unit_last(scales),
            "scales must be [E, N, K/group_size]")
     _check(n % block_n == 0, f"N={n} is not a multiple of block_n={block_n}")
     tail = _moe16_tail(c, a, sorted_ids, expert_ids, num_post_padded, topk_weights, top_k, block_m, silu_mul,
@@ -746,7 +751,7 @@ def _moe_fp8_w8a16(c, a, b, scales, sorted_ids, expert_ids, num_post_padded, top
     _check(n % block_n == 0, f"N={n} is not a multiple of block_n={block_n}")
     block = scales.dim() == 3 and tuple(scales.shape) == (e, (n + 127) // 128, k // 128) and scales.size(2) != 1
     if block:
-        _check(scales.dtype == torch.float32 and scales.stride(2) == 1, "block scales must be float32 [E, N/128, K/128]")
+        _check(scales.dtype == torch.float32 and _unit_last(scales), "block scales must be float32 [E, N/128, K/128]")
         s_es, s_ns, s_ks = scales.stride(0), scales.stride(1), scales.stride(2)
     else:
         scales, s_es, s_ns = _channel_scales(scales, e, n)
@@ -829,7 +834,7 @@ def _mxfp4_dense(w, x, scales, bias, cfg):
     _check(w.dtype == torch.uint8 and w.stride(1) == 1 and 2 * w.size(1) == k, "w must be uint8 [N, K/2]")
     _check(scales.dtype == torch.uint8, "scale must be uint8 (e8m0)")
     _check(k % 64 == 0, f"K must be a multiple of 64, got K={k}")
-    _check(tuple(scales.shape) == (n, k // 32) and scales.stride(1) == 1, "scales must be [N, K/32]")
+    _check(tuple(scales.shape) == (n, k // 32) and _unit_last(scales), "scales must be [N, K/32]")
     _check(x.dtype in (torch.bfloat16, torch.float16) and x.stride(1) == 1, "x must be bf16/fp16, contiguous in dim 1")
     m = x.size(0)
     out = torch.empty((m, n), dtype=x.dtype, device=x.device)
@@ -873,7 +878,7 @@ def mxfp4_dequant(w, scales):
     _check(w.dim() == 2 and w.dtype == torch.uint8 and w.stride(1) == 1, "w must be uint8 [N, K/2]")
     _check(scales.dtype == torch.uint8, "scale must be uint8 (e8m0)")
     n, k = w.size(0), 2 * w.size(1)
-    _check(tuple(scales.shape) == (n, k // 32) and scales.stride(1) == 1, "scales must be [N, K/32]")
+    _check(tuple(scales.shape) == (n, k // 32) and _unit_last(scales), "scales must be [N, K/32]")
     out = torch.empty((n, k), dtype=torch.bfloat16, device=w.device)
     _lib.call("strix_dequant_bf16", _lib.FMT_MXFP4, _ptr(w), w.stride(0), _ptr(scales), _lib.S_E8M0, scales.stride(0),
               32, 1, _ptr(out), k, n, k, _stream(w))
@@ -1032,7 +1037,7 @@ def w8a16_skinny_gemm(in_a, in_b, in_scale, in_bias, CuCount, group_size):
     _skinny_rows(in_b)
     if group_size:
         _check(k % group_size == 0, f"K must be divisible by group_size={group_size}")
-        _check(in_scale.dim() == 2 and tuple(in_scale.shape) == (n, k // group_size) and in_scale.stride(1) == 1,
+        _check(in_scale.dim() == 2 and tuple(in_scale.shape) == (n, k // group_size) and _unit_last(in_scale),
                f"Scale must be [{n}, {k // group_size}] but got {list(in_scale.shape)}")
         s_ns, s_ks = in_scale.stride(0), 1
     else:
@@ -1064,7 +1069,7 @@ def w8a16_gemm(in_a, in_b, in_scale, in_bias, group_size):
     _check(k % 64 == 0, f"K must be a multiple of 64, got K={k}")
     if group_size:
         _check(k % group_size == 0, f"K must be divisible by group_size={group_size}")
-        _check(in_scale.dim() == 2 and tuple(in_scale.shape) == (n, k // group_size) and in_scale.stride(1) == 1,
+        _check(in_scale.dim() == 2 and tuple(in_scale.shape) == (n, k // group_size) and _unit_last(in_scale),
                f"Scale must be [{n}, {k // group_size}] but got {list(in_scale.shape)}")
         s_ns, s_ks = in_scale.stride(0), 1
     else:
@@ -1095,7 +1100,7 @@ def fp8_skinny_gemm(in_a, in_b, in_scale, in_bias, CuCount):
     _check(in_b.size(1) == k and in_b.stride(1) == 1 and in_a.stride(1) == 1, "K mismatch or non-contiguous rows")
     _skinny_rows(in_b)
     if in_scale.dim() == 2:
-        _check(tuple(in_scale.shape) == (n, k // 128) and in_scale.stride(1) == 1 and k % 128 == 0,
+        _check(tuple(in_scale.shape) == (n, k // 128) and _unit_last(in_scale) and k % 128 == 0,
                f"Scale must be [{n}, {k // 128}] but got {list(in_scale.shape)}")
         s_ns, s_ks, kgroup = in_scale.stride(0), 1, 128
     else:
@@ -1121,7 +1126,7 @@ def mxfp4_gemv(x, w, scales):
     n = w.size(0)
     _check(1 <= m <= 8, "mxfp4_gemv is for M <= 8")
     _check(w.size(1) * 2 == k and k % 32 == 0, "K mismatch or K % 32")
-    _check(scales.dtype == torch.uint8 and tuple(scales.shape) == (n, k // 32) and scales.stride(1) == 1,
+    _check(scales.dtype == torch.uint8 and tuple(scales.shape) == (n, k // 32) and _unit_last(scales),
            "scales must be uint8 [N, K/32]")
     return _w16(_lib.FMT_MXFP4, w, x, scales, _lib.S_E8M0, scales.stride(0), 1, 32, 1, None)
 
@@ -1137,7 +1142,7 @@ def _int4_ex_checks(w, n_scales, k, group_size, scales):
     _check(w.size(1) * 2 == k and k % 64 == 0, "K mismatch or K % 64")
     _check(group_size % 32 == 0 and k % group_size == 0, "group_size % 32 and K % group")
     _check(scales.dtype == torch.bfloat16 and scales.dim() == 2 and tuple(scales.shape) == (n_scales, k // group_size)
-           and scales.stride(1) == 1, "scales must be bf16 [N, K / group_size]")
+           and _unit_last(scales), "scales must be bf16 [N, K / group_size]")
 
 
 # Reference schema: csrc/torch_ops.cpp:266-268: uint4b8 weights in the

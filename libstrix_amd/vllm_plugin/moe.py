@@ -322,7 +322,7 @@ def zp_layout_ok(w: torch.Tensor, z: torch.Tensor | None, group: int | None) -> 
         return False
     e, n, k2 = w.shape
     return (z.dtype == torch.uint8 and z.dim() == 3 and n % 2 == 0 and (2 * k2) % group == 0
-            and tuple(z.shape) == (e, n // 2, 2 * k2 // group) and z.stride(2) == 1)
+            and tuple(z.shape) == (e, n // 2, 2 * k2 // group) and (z.size(2) == 1 or z.stride(2) == 1))
 
 
 def wna16_bad(hidden_states, w1, w2, s1, s2, group, activation, expert_map, a1q_scale=None, a2_scale=None,
@@ -361,7 +361,7 @@ def mxfp4_bad(hidden_states, w1, w2, s1, s2, activation, expert_map, a1q_scale=N
     fused gate activation, no biases (the reference has no MXFP4 MoE chain)."""
     def scales_ok(w, s):
         return (s is not None and s.dtype == torch.uint8 and s.dim() == 3
-                and tuple(s.shape) == (w.size(0), w.size(1), 2 * w.size(2) // 32) and s.stride(2) == 1)
+                and tuple(s.shape) == (w.size(0), w.size(1), 2 * w.size(2) // 32) and (s.size(2) == 1 or s.stride(2) == 1))
 
     checks = {
         "2d": hidden_states.dim() == 2,
