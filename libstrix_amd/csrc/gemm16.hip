@@ -503,7 +503,7 @@ __global__ void __launch_bounds__(WAVES * 64) stream16_kernel(G16 p) {
 // kb+1 into LDS, so with one wave of each kind per SIMD the decode ALU work
 // runs under the MFMAs instead of in turn with them. NP == 0: every wave
 // decodes its share, then computes.
-template <int FMT, int BM, int BN, int WM, int WN, int NP, bool MOE, int EPI, int ACT, bool F16>
+template <int FMT, int BM, int BN, int WM, int WN, int NP, bool MOE, int EPI, int ACT, bool F16, bool RAWL = false>
 __global__ void __launch_bounds__((WM * WN + NP) * 64) tiled16_kernel(G16 p, int tiles_m, int tiles_n, int group_m) {
   constexpr int W = WM * WN;                 // MFMA waves
   constexpr int PW = NP > 0 ? NP : W;        // waves that load and decode
@@ -526,7 +526,25 @@ __global__ void __launch_bounds__((WM * WN + NP) * 64) tiled16_kernel(G16 p, int
   constexpr bool GATED = (EPI == kEpiGated);
   constexpr int NTH = GATED ? NT / 2 : NT;
   static_assert(!GATED || NT % 2 == 0, "gated wave tiles pair gate and up subtiles");
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * STAGE];
+  // RAWL: the packed 4-bit weights of a stage, with one 4-byte word of scale
+  // bits per row and one of zero-point bits per row pair, arrive by direct
+  // global->LDS copies into one of RS raw slots; producers decode from there.
+  // No producer load then targets a register, so no compiler-inserted wait
+  // can drain the copies in flight: each wait is the explicit count below.
+  constexpr bool ZPF = (FMT == kWInt4Zp);
+  constexpr int RS = RAWL ? 3 : 0;
+  constexpr int RAW_W = BN * 32;                    // 64 K of 4-bit values per row
+  constexpr int RAW_S = RAW_W;                      // scale words: BN x 4 bytes
+  constexpr int RAW_Z = RAW_S + BN * 4;             // zero-point words: BN/2 x 4 bytes
+  constexpr int RAWSLOT = RAW_Z + (ZPF ? BN * 2 : 0);
+  constexpr int RQ = RAWL ? BN / 32 : 0;            // 1 KiB raw weight copies per stage
+  constexpr int SQ = RAWL ? BN / 64 : 0;            // 4-byte-per-lane scale copies per stage
+  constexpr int ZQ = (RAWL && ZPF) ? BN / 128 + (BN % 128 ? 1 : 0) : 0;  // zero-point copies
+  static_assert(!RAWL || (BITS == 4 && NP > 0 && RQ % PW == 0 && SQ + ZQ <= PW && BN % 64 == 0),
+                "raw-in-LDS decode: 4-bit weights, producer waves, copies split evenly");
+  static_assert(STAGES * STAGE + RS * RAWSLOT <= 160 * 1024, "LDS budget");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[STAGES * STAGE + RS * RAWSLOT];
+  uint8_t* const rawbase = smem + STAGES * STAGE;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -623,35 +641,115 @@ __global__ void __launch_bounds__((WM * WN + NP) * 64) tiled16_kernel(G16 p, int
       g2l_b128(base + qoff[j], st + (DIRECT_W ? q : q + BN / 8) * 1024);
     }
   };
+  // One 16-byte raw piece with its scale bits and zero-point byte.
+  struct WBuf1 {
+    u32x4 w;
+    uint32_t s, z;
+  };
+  auto decode_piece = [&](uint8_t* st, int j, const WBuf1& b) {
+    const float sc = wscale_value<FMT>(p, b.s);
+    const float z = ZP ? (float)((pgrow[j] & 1) ? (b.z >> 4) : (b.z & 15)) : 8.0f;
+    uint32_t v[PV / 2];
+    constexpr int PAIRS_PER_DWORD = 32 / BITS / 2;
+    if constexpr (FMT == kWMxfp4 && !F16) {
+      if (scale_kind<FMT>(p) == kSE8m0 && mxfp4_lut_ok(b.s)) {
+        const Mxfp4Lut t = mxfp4_lut(b.s);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) mxfp4_dword_lut(b.w[i], t, &v[4 * i]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) decode_dword<FMT, F16>(b.w[i], sc, z, &v[i * PAIRS_PER_DWORD]);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) decode_dword<FMT, F16>(b.w[i], sc, z, &v[i * PAIRS_PER_DWORD]);
+    }
+    const int row = prow[j];
+#pragma unroll
+    for (int c = 0; c < PV / 8; ++c) {
+      const int chunk = pidx[j] * (PV / 8) + c;
+      u32x4 o;
+      o[0] = v[4 * c]; o[1] = v[4 * c + 1]; o[2] = v[4 * c + 2]; o[3] = v[4 * c + 3];
+      *reinterpret_cast<u32x4*>(st + row * 128 + 16 * (chunk ^ lds_swz(row))) = o;
+    }
+  };
   auto decode_w = [&](int buf, const WBuf& b) {
     uint8_t* st = smem + buf * STAGE;
 #pragma unroll
+    for (int j = 0; j < PPT; ++j) decode_piece(st, j, WBuf1{b.w[j], b.s[j], b.z[j]});
+  };
+
+  // ---- RAWL copies. Raw copy c of a stage: rows 32c..32c+31, lane l takes
+  // row 32c + l/2, bytes 16*(l&1) of its 32-byte stage slice (LDS slot order
+  // is row-major, so lane l lands at 16*l of the copy's KiB). Every producer
+  // wave also issues exactly one 4-byte-per-lane copy per stage: waves
+  // 0..SQ-1 the scale words of rows 64w..64w+63, wave SQ the zero-point words
+  // of row pairs 0..63 (int4 with zero points), the others repeat the last
+  // of these (same bytes to the same place), so every producer wave counts
+  // the same number of copies per stage.
+  constexpr int RQPW = RAWL ? RQ / PW : 0;
+  uint32_t roff[RQPW > 0 ? RQPW : 1];
+#pragma unroll
+  for (int j = 0; j < RQPW; ++j) {
+    const int c = pwave + PW * j;
+    const int row = 32 * c + (lane >> 1);
+    roff[j] = (uint32_t)min(wrow_of(row), p.N - 1) * (uint32_t)p.ldw + 16u * (uint32_t)(lane & 1);
+  }
+  const int nxq = SQ + ZQ;
+  const int xq = RAWL ? min(pwave, nxq - 1) : 0;     // this wave's 4-byte copy
+  const bool x_is_z = ZPF && xq >= SQ;
+  const int sbytes = scale_kind<FMT>(p) == kSF32 ? 4 : (scale_kind<FMT>(p) == kSE8m0 ? 1 : 2);
+  int64_t xrow = 0;   // element index of the row's (pair's) first scale (zero point)
+  if constexpr (RAWL) {
+    if (x_is_z) {
+      const int pr = 64 * (xq - SQ) + lane;           // LDS row pair
+      xrow = wzero_row(p, expert, min(wrow_of(2 * min(pr, BN / 2 - 1)), p.N - 1));
+    } else {
+      const int row = 64 * xq + lane;
+      xrow = wscale_row(p, expert, min(wrow_of(row), p.N - 1));
+    }
+  }
+  // Byte address of the K-group element of stage kb for the 4-byte copy.
+  auto x_addr = [&](int kb) -> const uint8_t* {
+    if (x_is_z) return p.wz + xrow + (int64_t)((kb * 64) / p.ws_kgroup) * p.wz_ks;
+    const int64_t idx = xrow + (int64_t)((kb * 64) / p.ws_kgroup) * p.ws_ks;
+    return static_cast<const uint8_t*>(p.ws) + idx * sbytes;
+  };
+  auto dma_raw = [&](int kb, int slot) {
+    uint8_t* rs = rawbase + slot * RAWSLOT;
+    const uint8_t* wb = wbase + (int64_t)kb * 32;
+#pragma unroll
+    for (int j = 0; j < RQPW; ++j) {
+      uint32_t o = roff[j];
+      asm volatile("" : "+v"(o));
+      g2l_b128(wb + o, rs + (pwave + PW * j) * 1024);
+    }
+    const uint8_t* a = x_addr(kb);
+    const uint8_t* aw = reinterpret_cast<const uint8_t*>(reinterpret_cast<uintptr_t>(a) & ~(uintptr_t)3);
+    g2l_b32(aw, rs + (x_is_z ? RAW_Z + (xq - SQ) * 256 : RAW_S + xq * 256));
+  };
+  // Decode of stage kb's raw slot into LDS buffer buf (same pieces as decode_w).
+  auto decode_raw = [&](int kb, int slot, int buf) {
+    const uint8_t* rs = rawbase + slot * RAWSLOT;
+    uint8_t* st = smem + buf * STAGE;
+    const int g = (kb * 64) / p.ws_kgroup;   // the stage's first K group
+#pragma unroll
     for (int j = 0; j < PPT; ++j) {
-      const float sc = wscale_value<FMT>(p, b.s[j]);
-      const float z = ZP ? (float)((pgrow[j] & 1) ? (b.z[j] >> 4) : (b.z[j] & 15)) : 8.0f;
-      uint32_t v[PV / 2];
-      constexpr int PAIRS_PER_DWORD = 32 / BITS / 2;
-      if constexpr (FMT == kWMxfp4 && !F16) {
-        if (scale_kind<FMT>(p) == kSE8m0 && mxfp4_lut_ok(b.s[j])) {
-          const Mxfp4Lut t = mxfp4_lut(b.s[j]);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) mxfp4_dword_lut(b.w[j][i], t, &v[4 * i]);
-        } else {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) decode_dword<FMT, F16>(b.w[j][i], sc, z, &v[i * PAIRS_PER_DWORD]);
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) decode_dword<FMT, F16>(b.w[j][i], sc, z, &v[i * PAIRS_PER_DWORD]);
-      }
       const int row = prow[j];
-#pragma unroll
-      for (int c = 0; c < PV / 8; ++c) {
-        const int chunk = pidx[j] * (PV / 8) + c;
-        u32x4 o;
-        o[0] = v[4 * c]; o[1] = v[4 * c + 1]; o[2] = v[4 * c + 2]; o[3] = v[4 * c + 3];
-        *reinterpret_cast<u32x4*>(st + row * 128 + 16 * (chunk ^ lds_swz(row))) = o;
+      WBuf1 b;
+      b.w = lds128(rs + row * 32 + 16 * pidx[j]);
+      const uint32_t sw = *reinterpret_cast<const uint32_t*>(rs + RAW_S + 4 * row);
+      const uintptr_t sa = reinterpret_cast<uintptr_t>(p.ws) + (uintptr_t)((srow[j] + (int64_t)g * p.ws_ks) * sbytes);
+      uint32_t sh = (uint32_t)(sa & 3u) * 8u;
+      if constexpr (FMT == kWMxfp4) sh += 8u * (uint32_t)pidx[j];   // two 32-K groups per stage, bytes in a row
+      b.s = sbytes == 4 ? sw : (sw >> sh) & (sbytes == 2 ? 0xffffu : 0xffu);
+      b.z = 0;
+      if constexpr (ZPF) {
+        const uint32_t zw = *reinterpret_cast<const uint32_t*>(rs + RAW_Z + 4 * (row >> 1));
+        const uintptr_t za = reinterpret_cast<uintptr_t>(p.wz) + (uintptr_t)(zrow[j] + (int64_t)g * p.wz_ks);
+        b.z = (zw >> ((uint32_t)(za & 3u) * 8u)) & 0xffu;
       }
+      decode_piece(st, j, b);
     }
   };
 
@@ -707,7 +805,32 @@ __global__ void __launch_bounds__((WM * WN + NP) * 64) tiled16_kernel(G16 p, int
   };
   // Iteration kb: copies of stage kb were issued at kb-2, followed by the raw
   // weights (and scale, zero-point loads) of kb+2 and the copies of kb+1.
-  constexpr int LPW = DIRECT_W ? 0 : PPT * (2 + (ZP ? 1 : 0));  // loads per stage of load_w
+  constexpr int LPW = DIRECT_W ? 0 : (RAWL ? RQPW + 1 : PPT * (2 + (ZP ? 1 : 0)));  // weight loads per stage
+  if constexpr (RAWL) {
+    // Iteration kb: stage kb's token copies and raw(kb+1) have landed; raw
+    // copies run three stages ahead of their decode, token copies two ahead
+    // of their use.
+    if (is_prod) {
+      dma_raw(0, 0);
+      copy_a(0, 0);
+      dma_raw(clampk(1), 1);
+      copy_a(clampk(1), 1);
+      dma_raw(clampk(2), 2);
+      wait_vmcnt<2 * LPW + CPW>();   // raw(0) and tokens(0)
+    }
+    lds_barrier();
+    if (is_prod) decode_raw(0, 0, 0);
+    for (int kb = 0; kb < nkb; ++kb) {
+      if (is_prod) wait_vmcnt<LPW + CPW>();   // raw(kb+1), tokens(kb)
+      lds_barrier();
+      if (is_prod) {
+        decode_raw(clampk(kb + 1), (kb + 1) % 3, (kb + 1) % STAGES);
+        dma_raw(clampk(kb + 3), (kb + 3) % 3);
+        copy_a(clampk(kb + 2), (kb + 2) % STAGES);
+      }
+      if (is_cons) compute(kb);
+    }
+  }
   auto body = [&](int kb, WBuf& wdec) {
     if (is_prod) {
       wait_vmcnt<LPW + CPW>();
@@ -721,22 +844,24 @@ __global__ void __launch_bounds__((WM * WN + NP) * 64) tiled16_kernel(G16 p, int
     }
     if (is_cons) compute(kb);
   };
-  WBuf wA, wB;  // raw weights of even / odd stages
-  if (is_prod) {
-    load_w(0, wA);
-    copy_a(0, 0);
-    wait_vmcnt<0>();
-    decode_w(0, wA);
-    load_w(clampk(1), wB);
-    copy_a(clampk(1), 1);
-    load_w(clampk(2), wA);
+  if constexpr (!RAWL) {
+    WBuf wA, wB;  // raw weights of even / odd stages
+    if (is_prod) {
+      load_w(0, wA);
+      copy_a(0, 0);
+      wait_vmcnt<0>();
+      decode_w(0, wA);
+      load_w(clampk(1), wB);
+      copy_a(clampk(1), 1);
+      load_w(clampk(2), wA);
+    }
+    int kb = 0;
+    for (; kb + 1 < nkb; kb += 2) {
+      body(kb, wB);
+      body(kb + 1, wA);
+    }
+    if (kb < nkb) body(kb, wB);
   }
-  int kb = 0;
-  for (; kb + 1 < nkb; kb += 2) {
-    body(kb, wB);
-    body(kb + 1, wA);
-  }
-  if (kb < nkb) body(kb, wB);
   // Copies of clamped stages may still be landing: none may outlive the block.
   wait_vmem();
   if (!is_cons) return;
@@ -820,20 +945,54 @@ int launch_stream16(const G16& p, int grid_y, hipStream_t st, const char* op) {
   return check_launch(op);
 }
 
-template <int FMT, int BM, int BN, int WM, int WN, int NP, bool MOE, int EPI, int ACT, bool F16>
-int launch_tiled16(const G16& p, int grid_y_moe, hipStream_t st, const char* op) {
+template <int FMT, int BM, int BN, int WM, int WN, int NP, bool MOE, int EPI, int ACT, bool F16, bool RAWL>
+int launch_tiled16_as(const G16& p, int grid_y_moe, hipStream_t st, const char* op) {
   constexpr int COLS = (EPI == kEpiGated) ? BN / 2 : BN;
   constexpr int THREADS = (WM * WN + NP) * 64;
   const int tiles_n = (p.n_out + COLS - 1) / COLS;
   if constexpr (MOE) {
-    hipLaunchKernelGGL((tiled16_kernel<FMT, BM, BN, WM, WN, NP, MOE, EPI, ACT, F16>), dim3(tiles_n, grid_y_moe),
+    hipLaunchKernelGGL((tiled16_kernel<FMT, BM, BN, WM, WN, NP, MOE, EPI, ACT, F16, RAWL>), dim3(tiles_n, grid_y_moe),
                        dim3(THREADS), 0, st, p, 0, tiles_n, 0);
   } else {
     const int tiles_m = (p.M + BM - 1) / BM;
-    hipLaunchKernelGGL((tiled16_kernel<FMT, BM, BN, WM, WN, NP, MOE, EPI, ACT, F16>), dim3(tiles_m * tiles_n),
+    hipLaunchKernelGGL((tiled16_kernel<FMT, BM, BN, WM, WN, NP, MOE, EPI, ACT, F16, RAWL>), dim3(tiles_m * tiles_n),
                        dim3(THREADS), 0, st, p, tiles_m, tiles_n, 8);
   }
   return check_launch(op);
+}
+
+// The raw-in-LDS producer path takes 4-bit weights whose per-stage scale
+// (and zero point) of a row is one element of one 4-byte word: MXFP4 with
+// e8m0 scales (two groups of 32 per 64-K stage, in adjacent bytes of a row
+// with an even stride), or int4 with 64- or 128-element groups and 2- or
+// 4-byte scales. It needs the three decoded stages plus three raw slots in
+// LDS.
+template <int FMT, int BM, int BN, int NP>
+constexpr bool raw_lds_fits() {
+  return FmtInfo<FMT>::bits == 4 && NP > 0 && FMT != kWInt4Ex && BN % 64 == 0 && (BN / 32) % NP == 0 &&
+         BN / 64 + (BN + 127) / 128 <= NP && (BN + BM) * 128 * 3 + 3 * (BN * 36 + BN * 2) <= 160 * 1024;
+}
+
+template <int FMT, int BM, int BN, int NP>
+bool raw_lds_ok(const G16& p) {
+  if constexpr (!raw_lds_fits<FMT, BM, BN, NP>()) return false;
+  else {
+    if (FMT == kWMxfp4) return p.ws_kind == kSE8m0 && p.ws_kgroup == 32 && p.ws_ks == 1 && p.ws_ns % 2 == 0 &&
+                               p.ws_es % 2 == 0 && (reinterpret_cast<uintptr_t>(p.ws) & 1u) == 0;
+    if (p.ws_kgroup != 64 && p.ws_kgroup != 128) return false;
+    const int sb = p.ws_kind == kSF32 ? 4 : 2;
+    return (p.ws_kind == kSF32 || p.ws_kind == kSBf16 || p.ws_kind == kSF16) &&
+           (reinterpret_cast<uintptr_t>(p.ws) % sb) == 0;
+  }
+}
+
+template <int FMT, int BM, int BN, int WM, int WN, int NP, bool MOE, int EPI, int ACT, bool F16>
+int launch_tiled16(const G16& p, int grid_y_moe, hipStream_t st, const char* op) {
+  if constexpr (raw_lds_fits<FMT, BM, BN, NP>()) {
+    if (raw_lds_ok<FMT, BM, BN, NP>(p))
+      return launch_tiled16_as<FMT, BM, BN, WM, WN, NP, MOE, EPI, ACT, F16, true>(p, grid_y_moe, st, op);
+  }
+  return launch_tiled16_as<FMT, BM, BN, WM, WN, NP, MOE, EPI, ACT, F16, false>(p, grid_y_moe, st, op);
 }
 
 template <int FMT, int EPI, int ACT, bool F16>

@@ -679,21 +679,24 @@ __global__ void __launch_bounds__(WM * WN * 64) tiled8_kernel(G8 p, int tiles_m,
   bool qis_w[QPW];
 #pragma unroll
   for (int j = 0; j < QPW; ++j) {
-    const int q = wave + W * j;
+    const int q = wave + W * j;           // wave-uniform (BN is a multiple of 8, so a copy
+    const bool is_w = q < BN / 8;         // holds weight rows only or token rows only)
     const int row = 8 * q + (lane >> 3);  // operand row: weights first, then tokens
     uint32_t off;
-    if (row < BN) {
+    if (is_w) {
       const int r = min(wrow_of(row >> 4) + (row & 15), p.N - 1);
       off = (uint32_t)r * (uint32_t)p.ldw;
-      qis_w[j] = true;
     } else {
       int br, orw;
       bool v;
       token_row<MOE>(p, m0 + (row - BN), br, orw, v);
       off = (uint32_t)br * (uint32_t)p.lda;
-      qis_w[j] = false;
     }
+    qis_w[j] = is_w;
     qoff[j] = off + 16 * ((lane & 7) ^ lds_swz(row));
+    // Keep the offset a 32-bit register: the copy adds it to a scalar base
+    // (saddr form), so no 64-bit per-lane address stays live across the loop.
+    asm("" : "+v"(qoff[j]));
   }
   // Fragment reads: lane l reads row 16*subtile + l%16, chunks l/16 (half 0)
   // and 4 + l/16 (half 1), at their swizzled slots.
@@ -727,7 +730,14 @@ __global__ void __launch_bounds__(WM * WN * 64) tiled8_kernel(G8 p, int tiles_m,
     const uint8_t* wb = wbase + (int64_t)kb * p.w_kbs;
     const uint8_t* ab = p.a + (int64_t)kb * 128;
 #pragma unroll
-    for (int j = 0; j < QPW; ++j) g2l_b128((qis_w[j] ? wb : ab) + qoff[j], st + (wave + W * j) * 1024);
+    for (int j = 0; j < QPW; ++j) {
+      // Re-pinned at each use so the compiler neither hoists a 64-bit
+      // zero-extended copy of the offset out of the loop (live registers)
+      // nor builds the address per lane: scalar base + 32-bit offset.
+      uint32_t o = qoff[j];
+      asm volatile("" : "+v"(o));
+      g2l_b128((qis_w[j] ? wb : ab) + o, st + (wave + W * j) * 1024);
+    }
     if (has_extra) {
       uint8_t* dst = wave < SA_COPIES ? st + SA_OFF + wave * 256 : st + SW_OFF + (wave - SA_COPIES) * 256;
       g2l_b32(xptr + (int64_t)kb * xstride, dst);
