@@ -87,12 +87,45 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
     return LIB
 
 
+TORCH_EXT_SRC = PKG / "torch_ext" / "strix_ops.cpp"
+TORCH_EXT = PKG / "_strix_torch.so"
+
+
+def build_torch_ext(verbose: bool = False) -> Path:
+    """The C++ torch.ops.strix registration (torch_ext/strix_ops.cpp): host
+    code only, compiled with the system C++ compiler against the installed
+    torch's headers and libraries, linked to _strix_amd.so (found next to it
+    at run time through an $ORIGIN rpath)."""
+    import torch
+
+    tdir = Path(torch.__file__).resolve().parent
+    cxx = shutil.which("g++") or shutil.which("c++")
+    if cxx is None:
+        raise RuntimeError("no C++ compiler for the torch extension")
+    abi = int(bool(torch._C._GLIBCXX_USE_CXX11_ABI))
+    tmp = TORCH_EXT.with_suffix(".so.tmp")
+    cmd = [cxx, "-O2", "-std=c++17", "-fPIC", "-shared", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+           "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", "-DTORCH_EXTENSION_NAME=strix_torch",
+           f"-I{tdir / 'include'}", f"-I{tdir / 'include' / 'torch' / 'csrc' / 'api' / 'include'}",
+           "-I/opt/rocm/include", f"-I{INCLUDE}", str(TORCH_EXT_SRC), "-o", str(tmp),
+           f"-L{tdir / 'lib'}", "-ltorch", "-ltorch_cpu", "-ltorch_hip", "-lc10", "-lc10_hip", "-lamdhip64",
+           f"-L{PKG}", "-l:_strix_amd.so", "-Wl,-rpath,$ORIGIN", "-Wl,--no-undefined"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"torch extension build failed:\n{res.stderr[-6000:]}")
+    os.replace(tmp, TORCH_EXT)
+    return TORCH_EXT
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("-j", type=int, default=None)
     ap.add_argument("-v", action="store_true")
     a = ap.parse_args()
     print(build(a.j, a.v))
+    print(build_torch_ext(a.v))
 
 
 if __name__ == "__main__":

@@ -2,11 +2,17 @@
 """torch.ops.strix.* on top of the C ABI.
 
 The reference registers its ops from C++ (csrc/torch_ops.cpp:179-344). Here
-the schemas are defined from Python with torch.library and each CUDA-key
-implementation is a thin call into libstrix_amd/_strix_amd.so through ctypes,
-on the current stream, with no host synchronization (so the ops are HIP-graph
-capturable). Reference schemas are kept byte-identical; the ops this build
-adds for the W8A8 and zero-point numerics are additive.
+the ops on the configurations' call chains (quantizers, W8A8 GEMMs, MoE
+router / align / combine / expert GEMMs) are registered from C++ as well:
+libstrix_amd/_strix_torch.so (torch_ext/strix_ops.cpp), loaded first, defines
+their schemas and CUDA-key impls under a device guard, so a call does not go
+through Python. The remaining ops (the reference's API-parity surface) are
+defined here with torch.library, each CUDA-key implementation a thin call
+into libstrix_amd/_strix_amd.so through ctypes. Every schema string is
+recorded in SCHEMAS (the C++ ones too; a test compares them with the
+registered schemas). Launches go on the current stream with no host
+synchronization, so the ops are HIP-graph capturable. Reference schemas are
+kept byte-identical; the ops this build adds are additive.
 
 Every op raises RuntimeError on a bad argument (message from the library) and
 when the library is not built; there is no CPU or PyTorch fallback.
@@ -14,22 +20,47 @@ when the library is not built; there is no CPU or PyTorch fallback.
 
 from __future__ import annotations
 
+from pathlib import Path
+
 import torch
 
 from libstrix_amd import _lib
 
-_LIB = torch.library.Library("strix", "DEF")
+TORCH_EXT = Path(__file__).with_name("_strix_torch.so")
+# The C++ registration, when built: it must load (a broken build raises).
+if TORCH_EXT.exists():
+    _lib.load()  # the kernels library the extension links against, by the same path
+    torch.ops.load_library(str(TORCH_EXT))
+
+_LIB = torch.library.Library("strix", "FRAGMENT")
 SCHEMAS: dict[str, str] = {}
+NATIVE_OPS: set[str] = set()   # ops whose schema and impl come from the C++ registration
 _ACT = {"silu": _lib.ACT_SILU, "gelu_tanh": _lib.ACT_GELU_TANH}
 
 
+def _registered(name: str) -> bool:
+    """Whether the C++ registration defines `name` with a CUDA-key impl."""
+    try:
+        return torch._C._dispatch_has_kernel_for_dispatch_key(f"strix::{name}", "CUDA")
+    except RuntimeError:   # no such operator yet
+        return False
+
+
 def _define(schema: str):
+    """Defines `schema` and registers the decorated function as its CUDA impl,
+    unless the C++ registration already provides the op (then the Python
+    function stays as the ctypes rendering of the same call, unused)."""
     name = schema.split("(", 1)[0]
     SCHEMAS[name] = schema
-    _LIB.define(schema)
+    native = _registered(name)
+    if native:
+        NATIVE_OPS.add(name)
+    else:
+        _LIB.define(schema)
 
     def deco(fn):
-        _LIB.impl(name, fn, "CUDA")
+        if not native:
+            _LIB.impl(name, fn, "CUDA")
         return fn
 
     return deco
