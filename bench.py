@@ -427,7 +427,7 @@ def main() -> None:
     from libstrix_amd import workloads
 
     if not libstrix_amd.library_available():
-        raise SystemExit("libstrix_amd/_strix_amd.so is not built (python -m libstrix_amd.build)")
+        raise SystemExit("libstrix_amd/_strix_amd.so is not built (python libstrix_amd/build.py)")
     S = torch.ops.strix
     timer = Timer(torch)
     log("bench: headline config 2, M=4096")

@@ -192,6 +192,26 @@ int strix_w16_gemm(int fmt, const uint8_t* w, int64_t ldw, const void* scales, i
 int strix_dequant_bf16(int fmt, const uint8_t* w, int64_t ldw, const void* scales, int s_kind, int64_t s_ld,
                        int64_t kgroup, int64_t nblock, uint16_t* out, int64_t ldo, int64_t N, int64_t K, void* stream);
 
+/* W4A8 on the int8 MFMA: int8 activations per (row, 128-group) x 4-bit weights
+ * (value q - 8) widened to int8 in the tile, an exact int32 sum per 128-group
+ * folded in fp32 with the activation and weight scales. w4a8_wmma_gemm
+ * (csrc/torch_ops.cpp:283; csrc/gemm/w8a8_wmma_gemm.hip:128-135 is the
+ * reference's W4 variant): weights [N, K/2] bytes, order 1 = nibble j of each
+ * word is k j, 2 = RDNAHybridW4A16 words (k 0 2 4 6 1 3 5 7); fp32 weight
+ * scales sw[n * sw_ns + g * sw_gs] per 128-group g (sw_gs 0: one per row). */
+int strix_w4a8_gemm(const int8_t* qa, int64_t lda, const float* sa, int64_t sa_ld, const uint8_t* w4, int64_t ldw,
+                    int order, const float* sw, int64_t sw_ns, int64_t sw_gs, void* out, int64_t ldo, int out_dtype,
+                    int64_t M, int64_t N, int64_t K, void* stream);
+/* moe_gemm_w4a8 (csrc/torch_ops.cpp:213-217; csrc/moe/moe_gemm_w4a8.hip:57-277):
+ * int4 experts [E, N, K/2] (low nibble = even k) with fp32 scales [E, N, K/128],
+ * int8 activations with fp32 scales [rows, K/128]; block_m 64, 128 or 256. */
+int strix_moe_gemm_w4a8(void* c, int64_t ldc, int c_dtype, const int8_t* qa, int64_t lda, const float* sa,
+                        int64_t sa_ld, const uint8_t* w4, int64_t w_es, int64_t ldw, const float* sw, int64_t sw_es,
+                        int64_t sw_ns, const int32_t* sorted_ids, int64_t sorted_len, const int32_t* expert_ids,
+                        int64_t num_blocks, const int32_t* num_post, const float* topk_weights, int64_t num_slots,
+                        int64_t top_k, int64_t block_m, int silu_mul, int activation, int64_t N, int64_t K,
+                        void* stream);
+
 /* ------------------------------------------------------------------ MoE plumbing
  * Router: softmax -> top-k -> optional renormalize (vLLM fused_topk, called at
  * python/strix_vllm/moe.py:181-184). ids by logit value, ties to the lower id. */

@@ -45,6 +45,8 @@ SIGNATURES: dict[str, list] = {
     "strix_fp8_w8a8_block_gemm_kmajor": [P, L, P, L, P, P, L, P, L, I, L, L, L, I, P],
     "strix_w8a8_int8_gemm": [P, L, P, P, L, P, P, L, I, L, L, L, I, P],
     "strix_w8a8_int8_group_gemm": [P, L, P, L, P, L, I, P, L, L, P, L, I, L, L, L, I, P],
+    "strix_w4a8_gemm": [P, L, P, L, P, L, I, P, L, L, P, L, I, L, L, L, P],
+    "strix_moe_gemm_w4a8": [P, L, I, P, L, P, L, P, L, L, P, L, L, P, L, P, L, P, P, L, L, L, I, I, L, L, P],
     "strix_moe_gemm_fp8_w8a8": [P, L, I, P, L, P, L, P, L, L, P, L, L, P, L, P, L, P, P, L, L, L, I, I, L, L, P],
     "strix_moe_gemm_fp8_w8a8_kmajor": [P, L, I, P, L, P, L, P, P, L, L, P, L, P, L, P, P, L, L, L, I, I, L, L, P],
     "strix_moe_gemm_mxfp4": [P, L, L, P, L, L] + MOE16,
@@ -88,7 +90,7 @@ def load() -> ctypes.CDLL:
         return _lib
     if not LIB_PATH.exists():
         _load_error = (
-            f"{LIB_PATH} is not built: run `python -m libstrix_amd.build` "
+            f"{LIB_PATH} is not built: run `python libstrix_amd/build.py` "
             "(libstrix_amd has no CPU or PyTorch fallback)"
         )
         raise RuntimeError(_load_error)

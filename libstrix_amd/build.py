@@ -6,7 +6,10 @@ reference's CMake build (CMakeLists.txt:4-25, build.sh:8-14), whose arch was
 gfx1151; this library is gfx950-only and carries no torch symbols, so a plain
 `hipcc -shared` is all it needs.
 
-    python -m libstrix_amd.build [-j N] [-v]
+    python libstrix_amd/build.py [-j N] [-v]
+
+(run as a script, not through the package: importing the package loads the
+built library, which may predate the sources)
 """
 
 from __future__ import annotations

@@ -608,6 +608,42 @@ __global__ void __launch_bounds__(64 * NW * KS) ring8_kernel(G8 p) {
   }
 }
 
+// ============================================================ int4 widening (W4A8)
+// 1/16 for W4 weights: their MFMA operands are 16 * (q - 8), so the int32
+// partial is 16 times the group sum (exact: |partial| < 2^24) and this
+// power-of-two factor restores it exactly.
+template <int W4>
+constexpr float kW4Unit = W4 ? 0.0625f : 1.0f;
+
+// One packed word of 8 4-bit values -> two words of int8 16 * (q - 8) in
+// ascending k. W4 == 1: nibble j of the word is k j (byte b: k 2b low, 2b+1
+// high). W4 == 2 (RDNAHybridW4A16): low nibbles of bytes 0..3 are k 0 4 1 5,
+// high nibbles k 2 6 3 7.
+template <int W4>
+__device__ __forceinline__ void widen_word(uint32_t w, uint32_t& lo, uint32_t& hi) {
+  const uint32_t L = ((w << 4) & 0xF0F0F0F0u) ^ 0x80808080u;  // low nibbles, as 16 * (q - 8)
+  const uint32_t H = (w & 0xF0F0F0F0u) ^ 0x80808080u;         // high nibbles
+  if constexpr (W4 == 1) {
+    lo = __builtin_amdgcn_perm(H, L, 0x05010400u);  // L0 H0 L1 H1: k 0 1 2 3
+    hi = __builtin_amdgcn_perm(H, L, 0x07030602u);  // L2 H2 L3 H3: k 4 5 6 7
+  } else {
+    lo = __builtin_amdgcn_perm(H, L, 0x06040200u);  // L0 L2 H0 H2: k 0 1 2 3
+    hi = __builtin_amdgcn_perm(H, L, 0x07050301u);  // L1 L3 H1 H3: k 4 5 6 7
+  }
+}
+// The 16 packed bytes of a lane's fragment (8 per 64-K half) -> the 32-byte
+// int8 fragment of the two 16x16x64 MFMAs.
+template <int W4>
+__device__ __forceinline__ v8i widen_int4(const uint2& h0, const uint2& h1) {
+  v8i r;
+  uint32_t a, b;
+  widen_word<W4>(h0.x, a, b); r[0] = (int)a; r[1] = (int)b;
+  widen_word<W4>(h0.y, a, b); r[2] = (int)a; r[3] = (int)b;
+  widen_word<W4>(h1.x, a, b); r[4] = (int)a; r[5] = (int)b;
+  widen_word<W4>(h1.y, a, b); r[6] = (int)a; r[7] = (int)b;
+  return r;
+}
+
 // ============================================================ tiled8
 // LDS stage: operand rows of 128 bytes (the stage's 128-K block), weight
 // rows 0..BN-1 then token rows, each row's 16-byte chunks XOR-swizzled
@@ -618,13 +654,21 @@ __global__ void __launch_bounds__(64 * NW * KS) ring8_kernel(G8 p) {
 // so a wave's outstanding copies retire strictly in issue order and
 // `s_waitcnt vmcnt(n)` with n = copies issued for later stages waits for
 // exactly one stage.
-template <int KIND, int BM, int BN, int WM, int WN, int STAGES, bool MOE, int EPI, int ACT, bool WX128>
+template <int KIND, int BM, int BN, int WM, int WN, int STAGES, bool MOE, int EPI, int ACT, bool WX128, int W4 = 0>
 __global__ void __launch_bounds__(WM * WN * 64) tiled8_kernel(G8 p, int tiles_m, int tiles_n, int group_m) {
   constexpr int W = WM * WN;
   constexpr int TM = BM / WM, TN = BN / WN;
   constexpr int MT = TM / 16, NT = TN / 16;
   constexpr int SA = BN / 16, SB = BM / 16;
-  constexpr int NQ = 2 * (SA + SB);  // 1 KiB operand copies per stage (8 rows each)
+  // W4 (int8 group kind only): 4-bit weights, 1 plain (low nibble = even k,
+  // value q - 8) or 2 RDNAHybridW4A16 word order. A stage then holds each
+  // weight row's 128-K block as 64 packed bytes (16 rows per 1 KiB copy,
+  // 16-byte chunks XOR-swizzled by (row >> 2) & 3); the fragment read widens
+  // the nibbles to int8 16 * (q - 8), exact, and the fold divides by 16.
+  static_assert(W4 == 0 || (KIND == kI8Group && !WX128), "int4 weights: int8 group kind only");
+  constexpr int WCOPIES = W4 ? SA : 2 * SA;          // 1 KiB weight copies per stage
+  constexpr int TOK_BASE = WCOPIES * 1024;           // token rows start here in a stage
+  constexpr int NQ = WCOPIES + 2 * SB;  // 1 KiB operand copies per stage (8 token rows each)
   static_assert(NQ % W == 0, "operand copies split evenly over the waves");
   constexpr int QPW = NQ / W;
   constexpr bool HAS_SA = (KIND != kI8Token);
@@ -679,21 +723,26 @@ __global__ void __launch_bounds__(WM * WN * 64) tiled8_kernel(G8 p, int tiles_m,
   bool qis_w[QPW];
 #pragma unroll
   for (int j = 0; j < QPW; ++j) {
-    const int q = wave + W * j;           // wave-uniform (BN is a multiple of 8, so a copy
-    const bool is_w = q < BN / 8;         // holds weight rows only or token rows only)
-    const int row = 8 * q + (lane >> 3);  // operand row: weights first, then tokens
+    const int q = wave + W * j;           // wave-uniform (a copy holds weight rows only
+    const bool is_w = q < WCOPIES;        // or token rows only)
     uint32_t off;
-    if (is_w) {
+    if (is_w && W4) {
+      const int row = 16 * q + (lane >> 2);  // 64-byte packed rows
       const int r = min(wrow_of(row >> 4) + (row & 15), p.N - 1);
-      off = (uint32_t)r * (uint32_t)p.ldw;
+      off = (uint32_t)r * (uint32_t)p.ldw + 16 * ((lane & 3) ^ ((row >> 2) & 3));
+    } else if (is_w) {
+      const int row = 8 * q + (lane >> 3);
+      const int r = min(wrow_of(row >> 4) + (row & 15), p.N - 1);
+      off = (uint32_t)r * (uint32_t)p.ldw + 16 * ((lane & 7) ^ lds_swz(row));
     } else {
+      const int trow = 8 * (q - WCOPIES) + (lane >> 3);  // token row of the block
       int br, orw;
       bool v;
-      token_row<MOE>(p, m0 + (row - BN), br, orw, v);
-      off = (uint32_t)br * (uint32_t)p.lda;
+      token_row<MOE>(p, m0 + trow, br, orw, v);
+      off = (uint32_t)br * (uint32_t)p.lda + 16 * ((lane & 7) ^ lds_swz(trow));
     }
     qis_w[j] = is_w;
-    qoff[j] = off + 16 * ((lane & 7) ^ lds_swz(row));
+    qoff[j] = off;
     // Keep the offset a 32-bit register: the copy adds it to a scalar base
     // (saddr form), so no 64-bit per-lane address stays live across the loop.
     asm("" : "+v"(qoff[j]));
@@ -800,7 +849,7 @@ __global__ void __launch_bounds__(WM * WN * 64) tiled8_kernel(G8 p, int tiles_m,
     v8i bf[MT];
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
-      const uint8_t* sub = st + (SA + wm * MT + t) * 2048;
+      const uint8_t* sub = st + TOK_BASE + (wm * MT + t) * 2048;
       bf[t] = cat8(lds128(sub + frag0), lds128(sub + frag1));
     }
     float sa_t[MT];
@@ -817,8 +866,18 @@ __global__ void __launch_bounds__(WM * WN * 64) tiled8_kernel(G8 p, int tiles_m,
       for (int t = 0; t < MT; ++t) c1[t] = sw * sa_t[t];
     }
     auto afrag = [&](int s) -> v8i {
-      const uint8_t* sub = st + aidx[s] * 2048;
-      return cat8(lds128(sub + frag0), lds128(sub + frag1));
+      if constexpr (W4) {
+        // Lane (r16, g4) needs k 16*g4 + [0,16) of each 64-K half: 8 packed
+        // bytes at 32*h + 8*g4, i.e. chunk 2h + g4/2 at offset 8*(g4 & 1).
+        const uint8_t* row = st + aidx[s] * 1024 + r16 * 64 + 8 * (g4 & 1);
+        const int sw4 = (r16 >> 2) & 3;
+        const uint2 h0 = *reinterpret_cast<const uint2*>(row + 16 * ((g4 >> 1) ^ sw4));
+        const uint2 h1 = *reinterpret_cast<const uint2*>(row + 16 * ((2 + (g4 >> 1)) ^ sw4));
+        return widen_int4<W4>(h0, h1);
+      } else {
+        const uint8_t* sub = st + aidx[s] * 2048;
+        return cat8(lds128(sub + frag0), lds128(sub + frag1));
+      }
     };
     // Software pipeline over the weight subtiles: the fragment of subtile
     // s+1 is read while subtile s runs its MFMAs, and the block-scale fold
@@ -866,7 +925,7 @@ __global__ void __launch_bounds__(WM * WN * 64) tiled8_kernel(G8 p, int tiles_m,
           for (int t = 0; t < MT; ++t)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-              const float v = (KIND == kFp8Block) ? prev_f[t][i] : (float)prev_i[t][i];
+              const float v = (KIND == kFp8Block) ? prev_f[t][i] : (float)prev_i[t][i] * kW4Unit<W4>;
               acc[s - 1][t][i] = fmaf(v, fold_c(prev_sw, t, i), acc[s - 1][t][i]);
             }
         } else {
@@ -874,7 +933,7 @@ __global__ void __launch_bounds__(WM * WN * 64) tiled8_kernel(G8 p, int tiles_m,
           for (int t = 0; t < MT; ++t)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-              const float v = (KIND == kFp8Block) ? prev_f[t][i] : (float)prev_i[t][i];
+              const float v = (KIND == kFp8Block) ? prev_f[t][i] : (float)prev_i[t][i] * kW4Unit<W4>;
               const float c = (KIND == kFp8Block) ? (ONE_SW ? prev_c1[t] : prev_sw[0] * prev_sa[t])
                                                   : prev_sw[i] * prev_sa[t];
               acc[NT - 1][t][i] = fmaf(v, c, acc[NT - 1][t][i]);
@@ -913,7 +972,7 @@ __global__ void __launch_bounds__(WM * WN * 64) tiled8_kernel(G8 p, int tiles_m,
     for (int t = 0; t < MT; ++t)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float v = (KIND == kFp8Block) ? prev_f[t][i] : (float)prev_i[t][i];
+        const float v = (KIND == kFp8Block) ? prev_f[t][i] : (float)prev_i[t][i] * kW4Unit<W4>;
         const float c = (KIND == kFp8Block) ? (ONE_SW ? prev_c1[t] : prev_sw[0] * prev_sa[t]) : prev_sw[i] * prev_sa[t];
         acc[NT - 1][t][i] = fmaf(v, c, acc[NT - 1][t][i]);
       }
@@ -1079,16 +1138,16 @@ int launch_ring_dense(const G8& p, hipStream_t st, const char* op) {
   return check_launch(op);
 }
 
-template <int KIND, int BM, int BN, int WM, int WN, int STAGES, bool MOE, int EPI, int ACT, bool WX128>
+template <int KIND, int BM, int BN, int WM, int WN, int STAGES, bool MOE, int EPI, int ACT, bool WX128, int W4 = 0>
 int launch_tiled(const G8& p, int grid_y_moe, hipStream_t st, const char* op) {
   constexpr int COLS = (EPI == kEpiGated) ? BN / 2 : BN;
   const int tiles_n = (p.n_out + COLS - 1) / COLS;
   if constexpr (MOE) {
-    hipLaunchKernelGGL((tiled8_kernel<KIND, BM, BN, WM, WN, STAGES, MOE, EPI, ACT, WX128>),
+    hipLaunchKernelGGL((tiled8_kernel<KIND, BM, BN, WM, WN, STAGES, MOE, EPI, ACT, WX128, W4>),
                        dim3(tiles_n, grid_y_moe), dim3(WM * WN * 64), 0, st, p, 0, tiles_n, 0);
   } else {
     const int tiles_m = (p.M + BM - 1) / BM;
-    hipLaunchKernelGGL((tiled8_kernel<KIND, BM, BN, WM, WN, STAGES, MOE, EPI, ACT, WX128>),
+    hipLaunchKernelGGL((tiled8_kernel<KIND, BM, BN, WM, WN, STAGES, MOE, EPI, ACT, WX128, W4>),
                        dim3(tiles_m * tiles_n), dim3(WM * WN * 64), 0, st, p, tiles_m, tiles_n, 8);
   }
   return check_launch(op);
@@ -1367,6 +1426,110 @@ int strix_w8a8_int8_group_gemm(const int8_t* qa, int64_t lda, const float* sa, i
   p.M = (int)M; p.N = (int)N; p.K = (int)K; p.n_out = (int)N;
   if (w_excess128) return dense_dispatch<kI8Group, kEpiStore, true>(p, as_stream(stream), op, cfg);
   return dense_dispatch<kI8Group, kEpiStore, false>(p, as_stream(stream), op, cfg);
+}
+
+}  // extern "C"
+
+namespace strix {
+namespace {
+
+// Checks shared by the W4A8 entry points: int8 activations [rows, lda >= K],
+// packed 4-bit weight rows of K/2 bytes (16-byte aligned strides).
+int check_w4a8(const char* op, int64_t rows, int64_t N, int64_t K, int64_t lda, int64_t ldw, const void* a,
+               const void* w) {
+  STRIX_REQUIRE(rows >= 0 && N >= 0 && K >= 0, "%s: negative size", op);
+  STRIX_REQUIRE(K % 128 == 0, "%s: K must be a multiple of 128, got K=%lld", op, (long long)K);
+  STRIX_REQUIRE(ldw * 2 >= K && ldw % 16 == 0, "%s: weight rows must hold K/2 bytes at a 16-byte multiple stride", op);
+  STRIX_REQUIRE(lda >= K && lda % 16 == 0, "%s: activation row stride must be >= K and a multiple of 16", op);
+  STRIX_REQUIRE(aligned(a, 16) && aligned(w, 16), "%s: operands must be 16-byte aligned", op);
+  STRIX_REQUIRE(rows <= INT32_MAX && N <= INT32_MAX && K <= INT32_MAX, "%s: sizes overflow 32-bit indexing", op);
+  STRIX_REQUIRE(fits_u32_rows(rows, lda, K) && fits_u32_rows(N, ldw, K / 2),
+                "%s: an operand spans more than 4 GiB (the kernels use 32-bit row offsets); split the call", op);
+  return STRIX_OK;
+}
+
+template <int W4>
+int w4a8_dense(const G8& p, hipStream_t st, const char* op) {
+  if (p.M <= 128) return launch_tiled<kI8Group, 128, 128, 2, 2, 3, false, kEpiStore, kActSilu, false, W4>(p, 0, st, op);
+  return launch_tiled<kI8Group, 256, 256, 4, 2, 2, false, kEpiStore, kActSilu, false, W4>(p, 0, st, op);
+}
+
+template <int EPI, int ACT>
+int w4a8_moe(const G8& p, int block_m, int num_blocks, hipStream_t st, const char* op) {
+  switch (block_m) {
+    case 64: return launch_tiled<kI8Group, 64, 128, 1, 4, 4, true, EPI, ACT, false, 1>(p, num_blocks, st, op);
+    case 128: return launch_tiled<kI8Group, 128, 128, 2, 2, 3, true, EPI, ACT, false, 1>(p, num_blocks, st, op);
+    case 256: return launch_tiled<kI8Group, 256, 256, 4, 2, 2, true, EPI, ACT, false, 1>(p, num_blocks, st, op);
+    default: return set_error(STRIX_ERR_INVALID, "%s: block_m must be 64, 128 or 256, got %d", op, block_m);
+  }
+}
+
+}  // namespace
+}  // namespace strix
+
+extern "C" {
+
+int strix_w4a8_gemm(const int8_t* qa, int64_t lda, const float* sa, int64_t sa_ld, const uint8_t* w4, int64_t ldw,
+                    int order, const float* sw, int64_t sw_ns, int64_t sw_gs, void* out, int64_t ldo, int out_dtype,
+                    int64_t M, int64_t N, int64_t K, void* stream) {
+  const char* op = "w4a8_wmma_gemm";
+  int rc = check_w4a8(op, M, N, K, lda, ldw, qa, w4);
+  if (rc) return rc;
+  STRIX_REQUIRE(order == 1 || order == 2, "%s: nibble order must be 1 (plain) or 2 (RDNAHybridW4A16), got %d", op,
+                order);
+  STRIX_REQUIRE(out_dtype == STRIX_BF16 || out_dtype == STRIX_F16, "%s: output must be bfloat16 or float16", op);
+  STRIX_REQUIRE(ldo >= N && ldo % 4 == 0 && aligned(out, 8), "%s: output rows must be >= N, 8-byte aligned", op);
+  STRIX_REQUIRE(sa != nullptr && sw != nullptr, "%s: scales are required", op);
+  if (M == 0 || N == 0) return STRIX_OK;
+  STRIX_ARCH_GATE();
+  G8 p = {};
+  p.w = w4; p.ldw = ldw; p.w_kbs = 64;
+  p.sw = sw; p.sw_ns = sw_ns; p.sw_ks = sw_gs;
+  p.a = reinterpret_cast<const uint8_t*>(qa); p.lda = lda; p.sa = sa; p.sa_rs = sa_ld; p.sa_ks = 1;
+  p.out = out; p.ldo = ldo; p.out_f16 = out_dtype == STRIX_F16;
+  p.M = (int)M; p.N = (int)N; p.K = (int)K; p.n_out = (int)N;
+  return order == 2 ? w4a8_dense<2>(p, as_stream(stream), op) : w4a8_dense<1>(p, as_stream(stream), op);
+}
+
+int strix_moe_gemm_w4a8(void* c, int64_t ldc, int c_dtype, const int8_t* qa, int64_t lda, const float* sa,
+                        int64_t sa_ld, const uint8_t* w4, int64_t w_es, int64_t ldw, const float* sw, int64_t sw_es,
+                        int64_t sw_ns, const int32_t* sorted_ids, int64_t sorted_len, const int32_t* expert_ids,
+                        int64_t num_blocks, const int32_t* num_post, const float* topk_weights, int64_t num_slots,
+                        int64_t top_k, int64_t block_m, int silu_mul, int activation, int64_t N, int64_t K,
+                        void* stream) {
+  const char* op = "moe_gemm_w4a8";
+  int rc = check_w4a8(op, num_slots, N, K, lda, ldw, qa, w4);
+  if (rc) return rc;
+  STRIX_REQUIRE(c_dtype == STRIX_BF16 || c_dtype == STRIX_F16, "%s: output must be bfloat16 or float16", op);
+  STRIX_REQUIRE(top_k >= 1, "%s: top_k must be >= 1", op);
+  STRIX_REQUIRE(w_es % 16 == 0, "%s: the expert stride of the weights must be a multiple of 16 bytes", op);
+  STRIX_REQUIRE(num_blocks * block_m >= sorted_len, "%s: expert_ids.numel() * block_m must cover sorted_ids", op);
+  STRIX_REQUIRE(N % 16 == 0, "%s: N must be a multiple of 16", op);
+  STRIX_REQUIRE(activation == kActSilu || activation == kActGeluTanh, "%s: unknown activation", op);
+  const int64_t n_out = silu_mul ? N / 2 : N;
+  STRIX_REQUIRE(ldc >= n_out && ldc % 4 == 0 && aligned(c, 8), "%s: output rows must be >= %lld, 8-byte aligned",
+                op, (long long)n_out);
+  // A gated tile holds BN/2 gate and BN/2 up rows: 64 each (block_m 64, 128), 128 (block_m 256).
+  const int64_t half_tile = block_m == 256 ? 128 : 64;
+  STRIX_REQUIRE(!silu_mul || (N / 2) % half_tile == 0, "%s: gated N/2 must be a multiple of %lld at block_m %lld",
+                op, (long long)half_tile, (long long)block_m);
+  if (num_blocks == 0 || num_slots == 0 || N == 0) return STRIX_OK;
+  STRIX_ARCH_GATE();
+  G8 p = {};
+  p.w = w4; p.ldw = ldw; p.w_es = w_es; p.w_kbs = 64;
+  p.sw = sw; p.sw_es = sw_es; p.sw_ns = sw_ns; p.sw_ks = 1;
+  p.a = reinterpret_cast<const uint8_t*>(qa); p.lda = lda; p.sa = sa; p.sa_rs = sa_ld; p.sa_ks = 1;
+  p.out = c; p.ldo = ldc; p.out_f16 = c_dtype == STRIX_F16;
+  p.M = (int)num_slots; p.N = (int)N; p.K = (int)K; p.n_out = (int)n_out; p.gate_off = (int)(N / 2);
+  p.sorted_ids = sorted_ids; p.sorted_len = sorted_len; p.expert_ids = expert_ids; p.num_post = num_post;
+  p.num_slots = (int)num_slots; p.top_k = (int)top_k; p.topk_w = topk_weights;
+  hipStream_t st = as_stream(stream);
+  const int nb = (int)num_blocks, bm = (int)block_m;
+  if (silu_mul) {
+    if (activation == kActGeluTanh) return w4a8_moe<kEpiGated, kActGeluTanh>(p, bm, nb, st, op);
+    return w4a8_moe<kEpiGated, kActSilu>(p, bm, nb, st, op);
+  }
+  return w4a8_moe<kEpiStore, kActSilu>(p, bm, nb, st, op);
 }
 
 }  // extern "C"

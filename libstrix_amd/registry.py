@@ -446,19 +446,21 @@ KERNELS: list[Kernel] = [
     Kernel(
         "w4a8_wmma_gemm",
         "w4a16",
-        "uint4b8 RDNAHybridW4A16 weights x activations quantized to int8 per (row, 128-group) in the op: the "
-        "int8 activations are dequantized to bf16 and the weights decoded to bf16 for bf16 MFMA. "
-        "K % 128 == 0, weight group 0, 32 or 128",
+        "uint4b8 RDNAHybridW4A16 weights x activations quantized to int8 per (row, 128-group) in the op: "
+        "nibbles widened to int8 in the tile, int8 MFMA, an exact int32 sum per 128-group folded in fp32 "
+        "with both scales (weight group 0 or 128); 32-element weight groups dequantize the int8 activations "
+        "for the int4 bf16-MFMA GEMM. K % 128 == 0",
         {"weight_bits": 4, "group_size": (0, 32, 128), "rows": Range(lo=1), "dtype": "bf16"},
     ),
     Kernel(
         "moe_gemm_w4a8",
         "moe_gemm_w4a8",
         "expert GEMM over the WNA16 int4 layout (low nibble = even k, q - 8, bf16/fp16 scales per 128-K group) "
-        "with int8 activations per (row, 128-group): activations dequantized to bf16, then the int4 "
-        "bf16-MFMA grouped GEMM with the fused act*mul / top-k weight epilogues",
+        "with int8 activations per (row, 128-group): nibbles widened to int8 in the tile, int8 MFMA, an "
+        "exact int32 sum per 128-group folded in fp32 with both scales, fused act*mul / top-k weight "
+        "epilogues; tiles 64x128, 64x256, 128x128, 256x256",
         {"silu_mul": True, **_BF16, "activation_dtype": "int8", "weight_dtype": "uint8", "weight_bits": 4,
-         "quant": "wna16", "group_size": (128,), "activation": ("silu", "gelu_tanh"), **_MOE_TILES},
+         "quant": "wna16", "group_size": (128,), "activation": ("silu", "gelu_tanh"), "block_m": (64, 128, 256)},
     ),
 ]
 

@@ -1214,8 +1214,12 @@ def _(w, scales, group_size):
 
 # Reference schema: csrc/torch_ops.cpp:283: uint4b8 RDNAHybridW4A16 weights,
 # activations quantized to int8 per (row, 128-group) inside the op, fp32
-# weight scales [N] (one group) or [G, N] / [N, G]. The int8 activations are
-# dequantized (q * s, bf16) and contracted with the decoded weights on bf16 MFMA.
+# weight scales [N] (one group) or [G, N] / [N, G]
+# (csrc/gemm/w8a8_wmma_gemm.hip:940-1000). Per-channel and 128-K weight
+# groups run on the int8 MFMA (strix_w4a8_gemm: int32 sums per 128-group,
+# folded in fp32 with both scales, as the reference's fold does); 32-K groups
+# (which change the weight scale inside an MFMA's 64-K step) dequantize the
+# int8 activations and run the int4 bf16-MFMA GEMM.
 @_define("w4a8_wmma_gemm(Tensor in_w4, Tensor in_act, Tensor in_scale) -> Tensor")
 def w4a8_wmma_gemm(in_w4, in_act, in_scale):
     _check(in_act.dim() == 2 and in_act.dtype == torch.bfloat16, "Activation must be bf16 [M, K]")
@@ -1239,15 +1243,24 @@ def w4a8_wmma_gemm(in_w4, in_act, in_scale):
                    f"Scale must be [G, N], [N, G] or [N={n}] but got {list(in_scale.shape)}")
             scale, s_ns, s_ks = in_scale, in_scale.stride(0), 1
         _check(group % 32 == 0, f"weight group ({group}) must be a multiple of 32")
+        if g == 1:
+            s_ks, group = 0, 0          # one group over K: per-channel
     x = in_act.contiguous()
+    st = _stream(x)
     q = torch.empty((m, k), dtype=torch.int8, device=x.device)
     sa = torch.empty((m, k // 128), dtype=torch.float32, device=x.device)
-    xd = torch.empty((m, k), dtype=torch.bfloat16, device=x.device)
-    st = _stream(x)
     if m:
         _lib.call("strix_int8_quant_group128", _ptr(x), _act_code(x), k, _ptr(q), k, _ptr(sa), k // 128, m, k, st)
+    w = in_w4.view(torch.uint8)
+    if group in (0, 128) and w.stride(0) % 16 == 0 and w.data_ptr() % 16 == 0:
+        out = torch.empty((m, n), dtype=torch.bfloat16, device=x.device)
+        _lib.call("strix_w4a8_gemm", _ptr(q), k, _ptr(sa), k // 128, _ptr(w), w.stride(0), 2, _ptr(scale), s_ns,
+                  s_ks, _ptr(out), n, _lib.BF16, m, n, k, st)
+        return out
+    xd = torch.empty((m, k), dtype=torch.bfloat16, device=x.device)
+    if m:
         _lib.call("strix_int8_dequant_group128", _ptr(q), k, _ptr(sa), k // 128, _ptr(xd), _lib.BF16, k, m, k, st)
-    return _w16(_lib.FMT_INT4_EX, in_w4.view(torch.uint8), xd, scale, _lib.S_F32, s_ns, s_ks, group, 1, None)
+    return _w16(_lib.FMT_INT4_EX, w, xd, scale, _lib.S_F32, s_ns, s_ks, group, 1, None)
 
 
 @_fake("w4a8_wmma_gemm")
@@ -1258,8 +1271,14 @@ def _(in_w4, in_act, in_scale):
 # Reference schema: csrc/torch_ops.cpp:213-217: int8 activations per (row,
 # 128-group) (moe_act_quant_i8) x int4 experts in the WNA16 layout (uint8
 # [E, N, K/2], low nibble = even k, value q - 8) with bf16/fp16 scales per
-# 128-K group. The activations are dequantized (q * s, bf16) and the experts
-# run on the int4 bf16-MFMA grouped GEMM.
+# 128-K group (csrc/moe/moe_gemm_w4a8.hip:371-463, the same checks). The
+# experts run on the int8 MFMA: nibbles widened to int8 in the tile, an exact
+# int32 sum per 128-group, folded in fp32 with sa and the (exactly widened)
+# weight scale. Tiles: the reference's three (block_m, block_n) pairs, and
+# 256 x 256.
+_W4A8_TILES = ((64, 256), (128, 128), (64, 128), (256, 256))
+
+
 @_define(
     "moe_gemm_w4a8(Tensor(a!) c, Tensor qa, Tensor sa, Tensor b, Tensor scales, "
     "Tensor sorted_ids, Tensor expert_ids, Tensor num_post_padded, "
@@ -1268,18 +1287,29 @@ def _(in_w4, in_act, in_scale):
 )
 def moe_gemm_w4a8(c, qa, sa, b, scales, sorted_ids, expert_ids, num_post_padded, topk_weights, top_k, block_m,
                   block_n, silu_mul=False, activation="silu"):
-    _check(qa.dtype == torch.int8 and qa.dim() == 2 and qa.stride(1) == 1, "qa must be int8 [rows, K]")
+    _check(qa.dtype == torch.int8 and sa.dtype == torch.float32 and b.dtype == torch.uint8
+           and scales.dtype in (torch.bfloat16, torch.float16) and c.dtype == torch.bfloat16,
+           "moe_gemm_w4a8: qa int8, sa fp32, w uint8, scales bf16/fp16, c bf16")
+    _check(qa.dim() == 2 and b.dim() == 3 and scales.dim() == 3 and c.dim() == 2, "moe_gemm_w4a8: ranks")
+    _check(qa.is_contiguous() and sa.is_contiguous() and b.stride(2) == 1 and _unit_last(scales)
+           and c.stride(1) == 1, "moe_gemm_w4a8: layouts")
     rows, k = qa.shape
-    _check(k % 128 == 0, f"K must be a multiple of 128, got K={k}")
-    _check(sa.dtype == torch.float32 and tuple(sa.shape) == (rows, k // 128) and sa.stride(1) == 1,
-           "sa must be float32 [rows, K/128]")
-    _check(c.dtype == torch.bfloat16, "c must be bfloat16")
-    a = torch.empty((rows, k), dtype=torch.bfloat16, device=qa.device)
-    if rows:
-        _lib.call("strix_int8_dequant_group128", _ptr(qa), qa.stride(0), _ptr(sa), sa.stride(0), _ptr(a), _lib.BF16,
-                  k, rows, k, _stream(qa))
-    moe_gemm_w4a16(c, a, b, scales, sorted_ids, expert_ids, num_post_padded, topk_weights, top_k, block_m, block_n,
-                   silu_mul, activation, 128)
+    e, n = b.size(0), b.size(1)
+    _check(b.size(2) * 2 == k and qa.size(1) == k and sa.numel() == rows * (k // 128),
+           "qa [rows, K], sa [rows, K/128], w [E, N, K/2]")
+    _check(c.size(1) == (n // 2 if silu_mul else n), "c shape mismatch")
+    _check(not silu_mul or (n % 2 == 0 and topk_weights is None), "silu_mul needs even N and no topk_weights")
+    _check(k % 128 == 0 and n % block_n == 0, "K % 128 and N % block_n")
+    _check(tuple(scales.shape) == (e, n, k // 128), "scales must be [E, N, K / 128]")
+    _check(b.stride(1) % 8 == 0 and b.stride(0) % 8 == 0, "w strides must be multiples of 8")
+    _check((block_m, block_n) in _W4A8_TILES, f"moe_gemm_w4a8: unsupported block_m/block_n {block_m}/{block_n}")
+    _moe_common(c, sorted_ids, expert_ids, num_post_padded, topk_weights, block_m)
+    code = _activation(activation)
+    sw = scales.float()            # bf16 / fp16 -> fp32 is exact
+    _lib.call("strix_moe_gemm_w4a8", _ptr(c), c.stride(0), _lib.BF16, _ptr(qa), k, _ptr(sa), k // 128, _ptr(b),
+              b.stride(0), b.stride(1), _ptr(sw), sw.stride(0), sw.stride(1), _ptr(sorted_ids), sorted_ids.numel(),
+              _ptr(expert_ids), expert_ids.numel(), _ptr(num_post_padded), _ptr(topk_weights), c.size(0), top_k,
+              block_m, int(silu_mul), code, n, k, _stream(qa))
 
 
 @_fake("moe_gemm_w4a8")

@@ -150,7 +150,7 @@ def register() -> None:
     import libstrix_amd
 
     if not libstrix_amd.library_available():
-        raise RuntimeError("libstrix_amd/_strix_amd.so is not built (python -m libstrix_amd.build)")
+        raise RuntimeError("libstrix_amd/_strix_amd.so is not built (python libstrix_amd/build.py)")
 
     from libstrix_amd.vllm_plugin import fp8, int8, linear, moe, mxfp4
 

@@ -13,6 +13,8 @@ import importlib
 import pytest
 import torch
 
+from libstrix_amd import torch_ops
+
 import libstrix_amd.vllm_plugin as plugin
 from libstrix_amd.vllm_plugin import fp8, int8, linear, moe, mxfp4
 
@@ -406,6 +408,16 @@ def test_router_weight_on_input_drops_w2_weights(rec):
     assert rec.calls == ["moe_align", "moe_gemm_bf16", "moe_gemm_bf16", "moe_sum"]
     assert rec.args[2][6] is None
     assert rec.args[1][0].data_ptr() == ws13.data_ptr()           # the w13 output lives in the caller's workspace
+
+
+def test_w4a8_blocks():
+    # 128 x 128 once the experts average 128 routed rows.
+    assert moe.w4a8_blocks(8192, 8, 128) == (128, 128)
+    assert moe.w4a8_blocks(2048, 8, 128) == (128, 128)
+    assert moe.w4a8_blocks(1024, 8, 128) == (64, 128)
+    for t in (1, 1024, 4096, 8192, 65536):
+        bm, bn = moe.w4a8_blocks(t, 8, 128)
+        assert (bm, bn) in torch_ops._W4A8_TILES   # tiles the op accepts
 
 
 @pytest.mark.parametrize("kind", ["sym", "zp", "w4a8"])

@@ -17,7 +17,7 @@ HOT = {"int8_quant_per_token", "fp8_quant_group128", "w8a8_scaled_mm", "fp8_w8a8
 
 
 def test_extension_built_and_loaded():
-    assert T.TORCH_EXT.exists(), "python -m libstrix_amd.build builds _strix_torch.so"
+    assert T.TORCH_EXT.exists(), "python libstrix_amd/build.py builds _strix_torch.so"
     assert HOT <= T.NATIVE_OPS
 
 
