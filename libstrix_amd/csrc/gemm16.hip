@@ -189,6 +189,20 @@ __device__ __forceinline__ void mxfp4_dword_lut(uint32_t d, const Mxfp4Lut& t, u
   out[3] = __builtin_amdgcn_perm(o23, e23, 0x07060302u);
 }
 
+// e8m0 exponents whose scaled e2m1 values are all normal bf16 numbers
+// (0.5 * 2^(b-127) >= 2^-126 and 6 * 2^(b-127) < 2^128): the products are
+// exact, so any correct conversion gives the same bits.
+__device__ __forceinline__ bool mxfp4_cvt_ok(uint32_t b) { return b >= 2u && b <= 252u; }
+// 8 e2m1 codes of d (nibble i = value i) -> 4 dwords of bf16 pairs scaled by
+// 2^(b-127), one gfx950 scaled fp4 -> bf16 conversion per byte.
+__device__ __forceinline__ void mxfp4_dword_cvt(uint32_t d, uint32_t b, uint32_t* out) {
+  const float sc = __uint_as_float(b << 23);
+  out[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, sc, 0));
+  out[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, sc, 1));
+  out[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, sc, 2));
+  out[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, sc, 3));
+}
+
 // Decodes one dword of packed weights (8 values for 4-bit formats, 4 for
 // 8-bit) into 16-bit values, appending to out[] as packed pairs.
 template <int FMT, bool F16>
@@ -339,6 +353,11 @@ __global__ void __launch_bounds__(WAVES * 64) stream16_kernel(G16 p) {
       if constexpr (FMT == kWMxfp4 && !F16) {
         // e8m0 scales: bf16 by table (v_perm), the scalar path only for the
         // rare exponents the table cannot take. A lane's dwords share a scale.
+        if (scale_kind<FMT>(p) == kSE8m0 && mxfp4_cvt_ok(sbits)) {
+#pragma unroll
+          for (int i = 0; i < ndw; ++i) mxfp4_dword_cvt(raw[i], sbits, &wv[4 * i]);
+          return;
+        }
         if (scale_kind<FMT>(p) == kSE8m0 && mxfp4_lut_ok(sbits)) {
           const Mxfp4Lut t = mxfp4_lut(sbits);
 #pragma unroll
@@ -652,7 +671,10 @@ __global__ void __launch_bounds__((WM * WN + NP) * 64) tiled16_kernel(G16 p, int
     uint32_t v[PV / 2];
     constexpr int PAIRS_PER_DWORD = 32 / BITS / 2;
     if constexpr (FMT == kWMxfp4 && !F16) {
-      if (scale_kind<FMT>(p) == kSE8m0 && mxfp4_lut_ok(b.s)) {
+      if (scale_kind<FMT>(p) == kSE8m0 && mxfp4_cvt_ok(b.s)) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) mxfp4_dword_cvt(b.w[i], b.s, &v[4 * i]);
+      } else if (scale_kind<FMT>(p) == kSE8m0 && mxfp4_lut_ok(b.s)) {
         const Mxfp4Lut t = mxfp4_lut(b.s);
 #pragma unroll
         for (int i = 0; i < 4; ++i) mxfp4_dword_lut(b.w[i], t, &v[4 * i]);
@@ -915,7 +937,11 @@ __global__ void __launch_bounds__(256) dequant_kernel(G16 p, uint16_t* out, int6
   bool done = false;
   if constexpr (FMT == kWMxfp4) {
     const uint32_t b = p.ws_kind == kSE8m0 ? wscale_raw<FMT>(p, wscale_row(p, 0, n), k) : 1u;
-    if (p.ws_kind == kSE8m0 && mxfp4_lut_ok(b)) {
+    if (p.ws_kind == kSE8m0 && mxfp4_cvt_ok(b)) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) mxfp4_dword_cvt(raw[j], b, &v[4 * j]);
+      done = true;
+    } else if (p.ws_kind == kSE8m0 && mxfp4_lut_ok(b)) {
       const Mxfp4Lut t = mxfp4_lut(b);
 #pragma unroll
       for (int j = 0; j < 4; ++j) mxfp4_dword_lut(raw[j], t, &v[4 * j]);

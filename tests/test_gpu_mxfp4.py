@@ -66,6 +66,21 @@ def test_one_hot_activations_are_the_dequantizer():
     assert torch.equal(out.t().float(), oracle.mxfp4_decode(w, s))
 
 
+@pytest.mark.parametrize("m", [8, 128])
+def test_one_hot_every_normal_exponent(m):
+    """Exponents 2..252 (every scaled value a normal bf16) and zero blocks,
+    through the GEMM's own weight decoder: exact."""
+    n, k = 256, 256
+    w, _ = _w(n, k, 7)
+    s = torch.randint(2, 253, (n, k // 32), generator=torch.Generator().manual_seed(8), dtype=torch.uint8)
+    s[:4, 0] = 0
+    x = torch.zeros(m, k, dtype=torch.bfloat16)
+    cols = torch.arange(m) % k
+    x[torch.arange(m), cols] = 1.0
+    out = torch.ops.strix.mxfp4_wmma_gemm(w.to(DEV), x.to(DEV), s.to(DEV), None).cpu()
+    assert torch.equal(out.float(), oracle.mxfp4_decode(w, s)[:, cols].t())
+
+
 def test_zero_block_scale_is_zero():
     n, k = 64, 128
     w, _ = _w(n, k, 4)
