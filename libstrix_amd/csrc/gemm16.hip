@@ -579,9 +579,7 @@ __global__ void __launch_bounds__((WM * WN + NP) * 64) tiled16_kernel(G16 p, int
   const int wm = wave % WM, wn = (wave / WM) % WN;
   int tm, tn, expert = 0;
   if constexpr (MOE) {
-    tn = blockIdx.x;
-    tm = blockIdx.y;
-    if (tm * BM >= *p.num_post) return;
+    if (!moe_tile(*p.num_post, BM, tm, tn)) return;
     expert = p.expert_ids[tm];
     if (expert < 0) return;
   } else {

@@ -696,9 +696,7 @@ __global__ void __launch_bounds__(WM * WN * 64) tiled8_kernel(G8 p, int tiles_m,
 
   int tm, tn, expert = 0;
   if constexpr (MOE) {
-    tn = blockIdx.x;
-    tm = blockIdx.y;
-    if (tm * BM >= *p.num_post) return;
+    if (!moe_tile(*p.num_post, BM, tm, tn)) return;
     expert = p.expert_ids[tm];
     if (expert < 0) return;
   } else {

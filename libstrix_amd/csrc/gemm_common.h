@@ -112,13 +112,23 @@ __device__ __forceinline__ void finish_float4(const P& p, int orow, int col0, co
   store4(p, orow, col0, v);
 }
 
-// Maps a dense block index to (tile_m, tile_n): the hardware deals block b to
-// XCD b % 8, so each XCD gets a contiguous run of tiles, walked in
-// group_m-tall columns (tiles sharing a weight column run back to back).
+// The hardware deals the blocks of a launch to the eight XCDs round robin
+// (linear block b runs on XCD b % 8), and each XCD has its own L2.
+// xcd_remap turns b into a logical block id such that each XCD gets a
+// contiguous run of logical ids, for any block count: XCDs below nblk % 8
+// take one more. A bijection of [0, nblk).
+__device__ __forceinline__ int xcd_remap(int b, int nblk) {
+  const int q = nblk >> 3, r = nblk & 7;
+  const int x = b & 7, j = b >> 3;
+  return (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + j;
+}
+
+// Maps a dense block index to (tile_m, tile_n): each XCD gets a contiguous
+// run of tiles, walked in group_m-tall columns (tiles sharing a weight
+// column run back to back).
 __device__ __forceinline__ void dense_tile(int bid, int tiles_m, int tiles_n, int group_m, int& tm, int& tn) {
   const int nblk = tiles_m * tiles_n;
-  int b = bid;
-  if ((nblk & 7) == 0) b = (b & 7) * (nblk >> 3) + (b >> 3);
+  const int b = xcd_remap(bid, nblk);
   const int per_group = group_m * tiles_n;
   const int grp = b / per_group;
   const int first_m = grp * group_m;
@@ -126,6 +136,24 @@ __device__ __forceinline__ void dense_tile(int bid, int tiles_m, int tiles_n, in
   const int in = b - grp * per_group;
   tm = first_m + in % gm;
   tn = in / gm;
+}
+
+// MoE tile (tm, tn) of this block in a grid of (column tiles, row tiles):
+// only the row tiles holding routed rows (num_post of them, in tiles of bm,
+// at most gridDim.y) are dealt out; blocks past them return false. Each XCD
+// gets a contiguous run of row-major tiles, so the column tiles of one row
+// tile (which read the same gathered token rows) and the row tiles of one
+// expert (which read the same weights) run under one L2.
+__device__ __forceinline__ bool moe_tile(int num_post, int bm, int& tm, int& tn) {
+  const int gx = (int)gridDim.x;
+  const int rows = min((num_post + bm - 1) / bm, (int)gridDim.y);
+  const int active = rows * gx;
+  const int b = (int)blockIdx.x + (int)blockIdx.y * gx;
+  if (b >= active) return false;
+  const int lg = xcd_remap(b, active);
+  tm = lg / gx;
+  tn = lg - tm * gx;
+  return true;
 }
 
 }  // namespace strix
