@@ -259,8 +259,17 @@ __device__ __forceinline__ void decode_dword(uint32_t d, float s, float z, uint3
 // 4-bit weights in 16 bytes (a 64-K tail of a K that is 64 mod 128 uses 8
 // bytes, PV 16), 16 for 8-bit, 8 for bf16. MFMA step j of the chunk pairs the
 // lane's values 8j..8j+7 with the same K positions of the token rows.
-template <int FMT, int NT, int MT, int WAVES, bool MOE, int EPI, int ACT, bool F16>
+// FOLD (int4 with one scale per 128-K chunk or per row): the MFMAs take the
+// raw codes as 16-bit numbers OFF + q (OFF 128 for bf16, 1024 for fp16, whose
+// mantissa then holds q itself, so a code becomes a 16-bit value with two
+// byte permutes), and each chunk's product is folded into the fp32
+// accumulator as s * (P - (OFF + z) * A), with A the chunk's token sums from
+// one more MFMA against ones. The per-element decode then costs about one
+// VALU operation instead of four; the weights enter the products exactly,
+// where the unfolded path first rounds (q - z) * s to 16 bits.
+template <int FMT, int NT, int MT, int WAVES, bool MOE, int EPI, int ACT, bool F16, bool FOLD = false>
 __global__ void __launch_bounds__(WAVES * 64) stream16_kernel(G16 p) {
+  static_assert(!FOLD || FMT == kWInt4Zp || FMT == kWInt4Sym, "folded decode: int4 weights");
   constexpr int BITS = FmtInfo<FMT>::bits;
   constexpr int PV = 128 / BITS;   // K values per lane per full chunk (16 bytes)
   constexpr int CK = 4 * PV;       // K per full chunk
@@ -271,8 +280,7 @@ __global__ void __launch_bounds__(WAVES * 64) stream16_kernel(G16 p) {
   const int m0 = blockIdx.y * (16 * MT);
   int expert = 0;
   if constexpr (MOE) {
-    if (m0 >= *p.num_post) return;
-    expert = p.expert_ids[blockIdx.y];
+    expert = moe_block_expert(p.num_post, p.expert_ids, m0);
     if (expert < 0) return;
   }
   const int nout0 = blockIdx.x * (16 * NTH);
@@ -415,6 +423,71 @@ __global__ void __launch_bounds__(WAVES * 64) stream16_kernel(G16 p) {
   };
   auto compute = [&](const Buf& b) {
     uint32_t wv[NT][PV / 2];
+    if constexpr (FOLD) {
+      constexpr uint32_t HI = F16 ? 0x64646464u : 0x43434343u;   // high byte of OFF + q
+      constexpr float OFF = F16 ? 1024.0f : 128.0f;
+      constexpr uint32_t ONE2 = F16 ? 0x3c003c00u : 0x3f803f80u;  // two 16-bit ones
+      float cs[NT], cz[NT];   // this lane's row: scale and -(OFF + z) * scale
+#pragma unroll
+      for (int s = 0; s < NT; ++s) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t d = b.w[s][i];
+          const uint32_t lo = d & 0x0f0f0f0fu, hi = (d >> 4) & 0x0f0f0f0fu;
+          const uint32_t x0 = __builtin_amdgcn_perm(hi, lo, 0x05010400u);  // codes of k 0..3
+          const uint32_t x1 = __builtin_amdgcn_perm(hi, lo, 0x07030602u);  // codes of k 4..7
+          wv[s][4 * i + 0] = __builtin_amdgcn_perm(HI, x0, 0x04010400u);
+          wv[s][4 * i + 1] = __builtin_amdgcn_perm(HI, x0, 0x04030402u);
+          wv[s][4 * i + 2] = __builtin_amdgcn_perm(HI, x1, 0x04010400u);
+          wv[s][4 * i + 3] = __builtin_amdgcn_perm(HI, x1, 0x04030402u);
+        }
+        const float sc = scale_of((b.s[s] >> b.ssh[s]) & smask);
+        const uint32_t zb = ZP ? (b.z[s] >> b.zsh[s]) & 0xffu : 0u;
+        const float z = ZP ? (float)((wrow[s] & 1) ? (zb >> 4) : (zb & 15u)) : 8.0f;
+        cs[s] = sc;
+        cz[s] = -(OFF + z) * sc;
+      }
+      v4f part[NT][MT], asum[MT];
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        asum[t] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < NT; ++s) part[s][t] = v4f{0.f, 0.f, 0.f, 0.f};
+      }
+      const u32x4 ones = {ONE2, ONE2, ONE2, ONE2};
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int j = 0; j < PV / 8; ++j) {
+#pragma unroll
+          for (int s = 0; s < NT; ++s) {
+            u32x4 wq;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) wq[i] = wv[s][4 * j + i];
+            if constexpr (F16)
+              part[s][t] = mfma_f16(__builtin_bit_cast(f16x8, wq), __builtin_bit_cast(f16x8, b.a[t][j]), part[s][t]);
+            else
+              part[s][t] = mfma_bf16(__builtin_bit_cast(bf16x8, wq), __builtin_bit_cast(bf16x8, b.a[t][j]), part[s][t]);
+          }
+          if constexpr (F16)
+            asum[t] = mfma_f16(__builtin_bit_cast(f16x8, ones), __builtin_bit_cast(f16x8, b.a[t][j]), asum[t]);
+          else
+            asum[t] = mfma_bf16(__builtin_bit_cast(bf16x8, ones), __builtin_bit_cast(bf16x8, b.a[t][j]), asum[t]);
+        }
+      // Element i of a lane's result is weight row 4*g4 + i of the subtile:
+      // its scale terms come from the lane that decoded that row (lane 4*g4 + i).
+#pragma unroll
+      for (int s = 0; s < NT; ++s)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float si = __shfl(cs[s], 4 * g4 + i, 64);
+          const float zi = __shfl(cz[s], 4 * g4 + i, 64);
+#pragma unroll
+          for (int t = 0; t < MT; ++t)
+            acc[s][t][i] = fmaf(zi, asum[t][i], fmaf(si, part[s][t][i], acc[s][t][i]));
+        }
+      return;
+    }
 #pragma unroll
     for (int s = 0; s < NT; ++s) {
       const uint32_t sbits = HAS_S ? (b.s[s] >> b.ssh[s]) & smask : 0u;
@@ -439,7 +512,7 @@ __global__ void __launch_bounds__(WAVES * 64) stream16_kernel(G16 p) {
     if (c < f1) compute(A);
   }
   // A 4-bit K that is 64 mod 128 ends with a half chunk (8 bytes per lane).
-  if constexpr (FMT != kWBf16 && BITS == 4) {
+  if constexpr (FMT != kWBf16 && BITS == 4 && !FOLD) {
     if (tail && c1 == nch && c0 < c1) {
       const int kc = nfull * CK + g4 * (PV / 2);
       uint32_t wv[NT][PV / 2];
@@ -964,6 +1037,14 @@ template <int FMT, int NT, int MT, int WAVES, bool MOE, int EPI, int ACT, bool F
 int launch_stream16(const G16& p, int grid_y, hipStream_t st, const char* op) {
   constexpr int NTH = (EPI == kEpiGated) ? NT / 2 : NT;
   const int grid_x = (p.n_out + 16 * NTH - 1) / (16 * NTH);
+  // int4 with one scale per 128-K chunk (or per row) and no 64-K tail: the folded decode.
+  if constexpr (FMT == kWInt4Zp || FMT == kWInt4Sym) {
+    if ((p.ws_kgroup == 128 || p.ws_kgroup == 0) && p.K % 128 == 0) {
+      hipLaunchKernelGGL((stream16_kernel<FMT, NT, MT, WAVES, MOE, EPI, ACT, F16, true>), dim3(grid_x, grid_y),
+                         dim3(WAVES * 64), 0, st, p);
+      return check_launch(op);
+    }
+  }
   hipLaunchKernelGGL((stream16_kernel<FMT, NT, MT, WAVES, MOE, EPI, ACT, F16>), dim3(grid_x, grid_y), dim3(WAVES * 64), 0,
                      st, p);
   return check_launch(op);
@@ -1026,7 +1107,8 @@ int moe16_dispatch(const G16& p, int block_m, int num_blocks, hipStream_t st, co
     case 16: {
       // Four K-split waves, or two when K holds fewer than 12 chunks (a
       // fourth wave would get none): C5's w2 (K=768, six chunks) 8.8 -> 7.0
-      // us at T=1, 25.2 -> 20.6 us at T=8; longer K is faster with four.
+      // us at T=1, 25.2 -> 20.6 us at T=8; longer K is faster with four
+      // (and than with eight: C5's w13 at T=1 11.4 vs 12.7 us).
       constexpr int CK = 4 * (128 / FmtInfo<FMT>::bits);
       if ((p.K + CK - 1) / CK < 12) return launch_stream16<FMT, NTS, 1, 2, true, EPI, ACT, F16>(p, num_blocks, st, op);
       return launch_stream16<FMT, NTS, 1, 4, true, EPI, ACT, F16>(p, num_blocks, st, op);
@@ -1045,7 +1127,8 @@ int dense16_dispatch(const G16& p, hipStream_t st, const char* op, int cfg) {
   if (cfg < 0) cfg = M <= 16 ? 0 : (M <= 32 ? 1 : (M <= 64 ? 2 : 3));
   switch (cfg) {
     // Two waves split K: fewer, longer waves stream better than eight (M=1
-    // MXFP4 17408x5120: 32.0 -> 26.0 us; FP8 W8A16: 27.5 -> 24.0 us).
+    // MXFP4 17408x5120: 32.0 -> 26.0 us; FP8 W8A16: 27.5 -> 24.0 us; on
+    // narrow N, 5760x2880 and 2048x7168, eight are no faster).
     case 0: return launch_stream16<FMT, 1, 1, 2, false, kEpiStore, kActSilu, F16>(p, (M + 15) / 16, st, op);
     case 1: return launch_stream16<FMT, 1, 2, 2, false, kEpiStore, kActSilu, F16>(p, (M + 31) / 32, st, op);
     case 2: return launch_stream16<FMT, 1, 4, 4, false, kEpiStore, kActSilu, F16>(p, (M + 63) / 64, st, op);

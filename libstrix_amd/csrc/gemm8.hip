@@ -122,8 +122,7 @@ __global__ void __launch_bounds__(256) stream8_kernel(G8 p) {
   const int m0 = blockIdx.y * (16 * MT);
   int expert = 0;
   if constexpr (MOE) {
-    if (m0 >= *p.num_post) return;
-    expert = p.expert_ids[blockIdx.y];
+    expert = moe_block_expert(p.num_post, p.expert_ids, m0);
     if (expert < 0) return;
   }
   const int nout0 = (blockIdx.x * NS + ns) * (16 * NTH);
@@ -401,8 +400,7 @@ __global__ void __launch_bounds__(64 * NW * KS) ring8_kernel(G8 p) {
   const int m0 = blockIdx.y * 16 * MT;
   int expert = 0;
   if constexpr (MOE) {
-    if (m0 >= *p.num_post) return;
-    expert = p.expert_ids[blockIdx.y];
+    expert = moe_block_expert(p.num_post, p.expert_ids, m0);
     if (expert < 0) return;
   }
   const int nout0 = (blockIdx.x * NW + wave) * (16 * NTH);

@@ -138,6 +138,17 @@ __device__ __forceinline__ void dense_tile(int bid, int tiles_m, int tiles_n, in
   tn = in / gm;
 }
 
+// Expert of a decode kernel's row block blockIdx.y (-1: no routed rows):
+// num_post and the block's expert id are loaded together, with no branch
+// between them (expert_ids holds one entry per block of the grid, so the
+// load is in bounds for every block), one memory round trip before the
+// weight addresses are known instead of two.
+__device__ __forceinline__ int moe_block_expert(const int32_t* num_post, const int32_t* expert_ids, int m0) {
+  const int np = *num_post;
+  const int ex = expert_ids[blockIdx.y];
+  return m0 < np ? ex : -1;
+}
+
 // MoE tile (tm, tn) of this block in a grid of (column tiles, row tiles):
 // only the row tiles holding routed rows (num_post of them, in tiles of bm,
 // at most gridDim.y) are dealt out; blocks past them return false. Each XCD

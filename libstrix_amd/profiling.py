@@ -111,6 +111,9 @@ WORKLOADS = {
                       _dense_bytes(16)),
     "c1_m32": ("config-1 int8 W8A8 GEMM, M=32 N=K=5120", _int8_decode,
                5120 * 5120 + 5120 * 4 + 32 * 5120 + 32 * 4 + 32 * 5120 * 2),
+    "c3_t1": ("config-3 FP8-block MoE, T=1", lambda: _moe("c3", 1), None),
+    "c4_t1": ("config-4 MXFP4 MoE, T=1", lambda: _moe("c4", 1), None),
+    "c5_t1": ("config-5 WNA16 MoE, T=1", lambda: _moe("c5", 1), None),
     "c3_t4096": ("config-3 FP8-block MoE, T=4096 (route, align, quant, w13, quant, w2, sum)",
                  lambda: _moe("c3", 4096), None),
     "c4_t2048": ("config-4 MXFP4 MoE, T=2048", lambda: _moe("c4", 2048), None),
