@@ -123,11 +123,13 @@ namespace {
 
 // out[s][b][j] (bf16 bits), j = 0,1: v_cvt_scalef32_pk_bf16_fp4 of byte b
 // (placed in byte lane `sel` of the source dword) with scale scales[s].
+// The pair is read as one 32-bit word: taking its elements one at a time
+// (r[0], r[1]) compiled to code that returned the low element twice.
 template <int SEL>
 __device__ void cvt_fp4_one(uint32_t b, float sc, uint16_t* o) {
-  const bf16x2_t r = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(b << (8 * SEL), sc, SEL);
-  o[0] = __builtin_bit_cast(uint16_t, r[0]);
-  o[1] = __builtin_bit_cast(uint16_t, r[1]);
+  const uint32_t r = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(b << (8 * SEL), sc, SEL));
+  o[0] = (uint16_t)(r & 0xffffu);
+  o[1] = (uint16_t)(r >> 16);
 }
 __global__ void probe_cvt_kernel(const float* scales, int nscales, uint16_t* fp4_out, float* fp8_out,
                                  uint16_t* bf16_out, const float* bf16_in, int nbf16) {

@@ -75,7 +75,7 @@ def test_hardware_converters():
     from pathlib import Path
 
     kat = json.loads((Path(__file__).parent / "golden" / "kat.json").read_text())
-    exps = [1, 100, 120, 127, 128, 200, 254]
+    exps = [1, 2, 100, 120, 127, 128, 200, 252, 254]
     scales = torch.tensor([2.0 ** (e - 127) for e in exps], dtype=torch.float32)
     x = torch.randn(4096, generator=torch.Generator().manual_seed(0)) * torch.logspace(-38, 38, 4096)
     x[:4] = torch.tensor([float("inf"), float("-inf"), 1.0 + 2.0**-8, 1.0 + 3 * 2.0**-8])
@@ -89,12 +89,14 @@ def test_hardware_converters():
     print("fp8 converter mismatches:", (got8[fin] != want8[fin]).nonzero().flatten().tolist()[:8])
     assert torch.equal(got8[fin], want8[fin]) and torch.isnan(got8[~fin]).all()
     assert torch.equal(b16.cpu().view(torch.bfloat16), x.to(torch.bfloat16))
-    # The scaled fp4 converter is recorded, not relied on: it does not follow the
-    # (low nibble, high nibble) -> (element 0, element 1) reading of the byte
-    # (byte 0x01 gives two copies of the low-nibble value), so the MXFP4
-    # decoders use their own exact e2m1 decode.
-    bad = 0
-    for si, sc in enumerate(scales.tolist()):
+    # The scaled fp4 converter (which the MXFP4 decoders use for e8m0
+    # exponents 2..252) follows the (low nibble, high nibble) -> (element 0,
+    # element 1) reading of every byte in every byte lane, exactly, wherever
+    # the scaled values are normal bf16 numbers (exponents 1 and 254 are
+    # outside that range and not checked).
+    for si, (e, sc) in enumerate(zip(exps, scales.tolist())):
+        if not 2 <= e <= 252:
+            continue
         want = (torch.stack([lut[codes & 15], lut[codes >> 4]], dim=-1) * sc).to(torch.bfloat16).float()
-        bad += int((fp4[si] != want[None]).any(dim=-1).sum())
-    print("fp4 converter: mismatching (scale, byte lane, byte) cases:", bad)
+        bad = int((fp4[si] != want[None]).any(dim=-1).sum())
+        assert bad == 0, f"fp4 converter: {bad} (byte lane, byte) mismatches at exponent {e}"
