@@ -297,6 +297,56 @@ def point_moe16(torch, S, timer, name, t, d, run, bytes_per_expert, e, top_k, h,
     return res
 
 
+def point_w4a8(torch, S, timer, t):
+    """W4A8 beside W4A16 on the config-5 expert shapes (E=128, top-8, hidden
+    2048, intermediate 768, symmetric int4 experts with bf16 scales per 128-K
+    group): the expert GEMMs of one layer (w13 gated + w2 weighted) with the
+    tile the plugin picks for each, after a shared route + align. W4A8 also
+    times its two int8 activation quantizers; W4A16 runs on bf16 tokens."""
+    from libstrix_amd.vllm_plugin import moe as pm
+
+    e, top_k, h, inter = 128, 8, 2048, 768
+    g = torch.Generator().manual_seed(900 + t)
+    w13 = torch.randint(0, 256, (e, 2 * inter, h // 2), generator=g, dtype=torch.uint8).cuda()
+    s13 = (torch.rand(e, 2 * inter, h // 128, generator=g) * 0.02 + 0.001).to(torch.bfloat16).cuda()
+    w2 = torch.randint(0, 256, (e, h, inter // 2), generator=g, dtype=torch.uint8).cuda()
+    s2 = (torch.rand(e, h, inter // 128, generator=g) * 0.02 + 0.001).to(torch.bfloat16).cuda()
+    x = torch.randn(t, h, generator=g).to(torch.bfloat16).cuda()
+    ids, wts = S.moe_route_topk(torch.randn(t, e, generator=g).cuda(), top_k, True)
+    slots = t * top_k
+    c13 = torch.empty(slots, inter, dtype=torch.bfloat16, device="cuda")
+    c2 = torch.empty(slots, h, dtype=torch.bfloat16, device="cuda")
+    qx = torch.empty(t, h, dtype=torch.int8, device="cuda")
+    sx = torch.empty(t, h // 128, dtype=torch.float32, device="cuda")
+    qi = torch.empty(slots, inter, dtype=torch.int8, device="cuda")
+    si_ = torch.empty(slots, inter // 128, dtype=torch.float32, device="cuda")
+    w = wts.reshape(-1)
+    bm8, bn8 = pm.w4a8_blocks(t, top_k, e)
+    a8 = S.moe_align(ids, e, bm8)
+
+    def run8(_i):
+        S.moe_act_quant_i8(x, qx, sx)
+        S.moe_gemm_w4a8(c13, qx, sx, w13, s13, *a8, None, top_k, bm8, bn8, True, "silu")
+        S.moe_act_quant_i8(c13, qi, si_)
+        S.moe_gemm_w4a8(c2, qi, si_, w2, s2, *a8, w, 1, bm8, bn8, False, "silu")
+
+    bm16, bn16 = pm.wna16_blocks(t, 2 * inter, h, top_k, e)
+    a16 = S.moe_align(ids, e, bm16)
+
+    def run16(_i):
+        S.moe_gemm_w4a16(c13, x, w13, s13, *a16, None, top_k, bm16, bn16, True, "silu", 128)
+        S.moe_gemm_w4a16(c2, c13, w2, s2, *a16, w, 1, bm16, bn16, False, "silu", 128)
+
+    us8 = timer(run8, iters=10)
+    us16 = timer(run16, iters=10)
+    ops = 2.0 * slots * (2 * inter * h + h * inter)
+    return {"T": t, "w4a8_us": round(us8, 1), "w4a8_tops": round(ops / us8 / 1e6, 1),
+            "w4a8_frac_int8_mfma": round(ops / us8 / 1e6 / PEAK_INT8_TOPS, 4), "w4a8_tiles": [bm8, bn8],
+            "w4a16_us": round(us16, 1), "w4a16_tflops": round(ops / us16 / 1e6, 1),
+            "w4a16_frac_bf16_mfma": round(ops / us16 / 1e6 / PEAK_BF16_TFLOPS, 4), "w4a16_tiles": [bm16, bn16],
+            "speedup": round(us16 / us8, 3)}
+
+
 def _cpu_model() -> str:
     """The host CPU's model name (lscpu's "Model name", read from /proc/cpuinfo)."""
     try:
@@ -483,6 +533,8 @@ def main() -> None:
         points["c5_wna16_moe"] = [point_moe16(torch, S, timer, "c5", t, c5, run5, per5, 128, 8, 2048, 768)
                                   for t in (1, 8192)]
         del c5
+        log("bench: W4A8 beside W4A16 on the config-5 expert shapes")
+        points["c5_w4a8_vs_w4a16_experts"] = [point_w4a8(torch, S, timer, t) for t in (2048, 8192)]
         out["points"] = points
     del h
     if not args.no_cpu:
