@@ -71,6 +71,8 @@ struct G16 {
   const int32_t* num_post;
   int num_slots, top_k;
   const float* topk_w;
+  int64_t a_rows;    // MoE: activation rows (for the 32-bit offset check of ring16)
+  int ring16;        // MoE int4 decode: 1 = through ring16 where it applies
 };
 
 // Scale of weight row n (within an expert) at K position k.
@@ -578,6 +580,245 @@ __global__ void __launch_bounds__(WAVES * 64) stream16_kernel(G16 p) {
       }
       finish_float4<EPI, ACT, MOE>(p, orow[t], col0, g, u);
     }
+}
+
+// ============================================================ ring16
+// int4 expert decode (MoE block_m 16) through an LDS ring, the 16-bit
+// counterpart of ring8. One wave owns NT = 2 weight subtiles (a gated
+// gate/up pair, or two plain subtiles) of one expert block over a range of
+// K; KS waves of a block split K, each with its own ring, and add their
+// partial sums through LDS at the end in a fixed order. Each ring slot is a
+// 256-K step filled by direct global->LDS copies: whole 128-byte lines of
+// packed weights (8 rows per copy, chunks XOR-swizzled like ring8), the
+// step's TQ token rows (512 bytes of bf16/fp16 each, 2 rows per copy,
+// swizzled by row), and one 4-byte-per-lane copy of the step's two 128-K
+// scale elements per weight row (lanes 0..31) and zero-point bytes per row
+// pair (lanes 32..47). Every wave issues the same copies per step, so
+// `s_waitcnt vmcnt` counts exactly the steps still in flight.
+//
+// Within a 128-K group lane (r16, g4) takes the 32 contiguous K of bytes
+// 16*g4.. of its row (one 16-byte LDS read) and MFMA j of the group the 8 K
+// of dword j; the token operand follows the same K order. The codes enter
+// the MFMA as OFF + q and each group is folded as s * (P - (OFF + z) * A),
+// A being the group's token sums from MFMAs against ones (the folded decode
+// of stream16). Scales must be bf16/fp16 with 128-element groups and K a
+// multiple of 256; the host checks this and the alignments.
+__device__ __forceinline__ int tok_swz(int row) { return row & 15; }
+
+template <int FMT, int TQ, int KS, int R, int EPI, int ACT, bool F16>
+__global__ void __launch_bounds__(64 * KS) ring16_kernel(G16 p) {
+  static_assert(FMT == kWInt4Zp || FMT == kWInt4Sym, "int4 weights");
+  static_assert(TQ == 2 || TQ == 8 || TQ == 16, "token rows per slot");
+  constexpr bool ZP = (FMT == kWInt4Zp);
+  constexpr bool GATED = (EPI == kEpiGated);
+  constexpr int NT = 2;
+  constexpr int NTH = GATED ? 1 : 2;
+  constexpr int WQ = 2 * NT;                 // weight copies per step (8 rows x 128 B)
+  constexpr int TC = TQ / 2;                 // token copies per step (2 rows x 512 B)
+  constexpr int PER = WQ + TC + 1;           // copies per step and wave
+  constexpr int T_OFF = NT * 2048;
+  constexpr int S_OFF = T_OFF + TQ * 512;
+  constexpr int SLOT = S_OFF + 256;
+  static_assert((R - 2) * PER < 64, "vmcnt counts at most 63 copies");
+  static_assert(KS == 1 || R * SLOT >= NT * 4 * 64 * 4, "a wave's ring holds its partial sums");
+  constexpr float OFF = F16 ? 1024.0f : 128.0f;
+  constexpr uint32_t HI = F16 ? 0x64646464u : 0x43434343u;
+  constexpr uint32_t ONE2 = F16 ? 0x3c003c00u : 0x3f803f80u;
+  __shared__ __attribute__((aligned(1024))) uint8_t ring_all[KS * R * SLOT];
+
+  const int lane = threadIdx.x & 63;
+  const int kw = KS == 1 ? 0 : __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  uint8_t* ring = ring_all + kw * (R * SLOT);
+  const int r16 = lane & 15, g4 = lane >> 4;
+  const int m0 = blockIdx.y * 16;
+  const int expert = moe_block_expert(p.num_post, p.expert_ids, m0);
+  if (expert < 0) return;
+  const int nout0 = blockIdx.x * (16 * NTH);
+  int wrow0[NT];
+  wrow0[0] = nout0;
+  wrow0[1] = GATED ? p.gate_off + nout0 : nout0 + 16;
+  const uint8_t* wbase = p.w + (int64_t)expert * p.w_es;
+
+  // Weight copy q: subtile q/2, rows 8*(q%2) + lane/8 of it; LDS position
+  // lane%8 of the row holds the row's 16-byte chunk (lane%8) ^ swz(row).
+  const int crow = lane >> 3;
+  uint32_t woff[WQ];
+#pragma unroll
+  for (int q = 0; q < WQ; ++q) {
+    const int row = 8 * (q & 1) + crow;
+    const int wr = min(wrow0[q >> 1] + row, p.N - 1);
+    woff[q] = (uint32_t)wr * (uint32_t)p.ldw + 16u * (uint32_t)((lane & 7) ^ lds_swz(row));
+  }
+  // Token copy c: rows 2c + lane/32, chunk (lane%32) ^ tok_swz(row) of the row's 512 bytes.
+  const uint8_t* abase = reinterpret_cast<const uint8_t*>(p.a);
+  uint32_t toff[TC];
+#pragma unroll
+  for (int c = 0; c < TC; ++c) {
+    const int row = 2 * c + (lane >> 5);
+    int br, orw;
+    bool v;
+    token_row<true>(p, m0 + row, br, orw, v);
+    toff[c] = (uint32_t)br * (uint32_t)(p.lda * 2) + 16u * (uint32_t)((lane & 31) ^ tok_swz(row));
+  }
+  // Scale / zero-point word of this lane (element index of the step-0 word).
+  const int srow_l = min(wrow0[(lane >> 4) & 1] + r16, p.N - 1);  // lanes 0..31: subtile lane/16, row lane%16
+  const uint16_t* sbase = static_cast<const uint16_t*>(p.ws);
+  const int64_t sidx = wscale_row(p, expert, srow_l);
+  int64_t zidx = 0;
+  if constexpr (ZP) {
+    const int q = lane & 15;                                          // lanes 32..47 (and 48..63 again)
+    const int zr = min(wrow0[q >> 3] + 2 * (q & 7), p.N - 2);
+    zidx = wzero_row(p, expert, zr);
+  }
+  const bool zlane = ZP && lane >= 32;
+  auto x_addr = [&](int st) -> const void* {
+    if (zlane) {
+      const uint8_t* za = p.wz + zidx + (int64_t)(2 * st) * p.wz_ks;
+      return reinterpret_cast<const void*>(reinterpret_cast<uintptr_t>(za) & ~(uintptr_t)3);
+    }
+    return sbase + sidx + (int64_t)(2 * st) * p.ws_ks;
+  };
+
+  auto issue = [&](int st, int slot) {
+    uint8_t* dst = ring + slot * SLOT;
+    const uint8_t* wb = wbase + (int64_t)st * 128;
+    const uint8_t* ab = abase + (int64_t)st * 512;
+#pragma unroll
+    for (int q = 0; q < WQ; ++q) {
+      uint32_t o = woff[q];
+      asm volatile("" : "+v"(o));
+      g2l_b128(wb + o, dst + q * 1024);
+    }
+#pragma unroll
+    for (int c = 0; c < TC; ++c) {
+      uint32_t o = toff[c];
+      asm volatile("" : "+v"(o));
+      g2l_b128(ab + o, dst + T_OFF + c * 1024);
+    }
+    g2l_b32(x_addr(st), dst + S_OFF);
+  };
+
+  const int trow = TQ == 16 ? r16 : (r16 & (TQ - 1));   // token row this lane reads
+  v4f acc[NT];
+#pragma unroll
+  for (int s2 = 0; s2 < NT; ++s2) acc[s2] = v4f{0.f, 0.f, 0.f, 0.f};
+  const u32x4 ones = {ONE2, ONE2, ONE2, ONE2};
+  const int skind = p.ws_kind;
+  auto sval = [&](uint32_t h) { return skind == kSF16 ? f16_bits_to_f32(h) : bf16_bits_to_f32(h); };
+
+  const int nst_all = p.K >> 8;
+  const int st0 = KS == 1 ? 0 : kw * nst_all / KS;
+  const int st1 = KS == 1 ? nst_all : (kw + 1) * nst_all / KS;
+#pragma unroll
+  for (int s0 = 0; s0 < R - 1; ++s0)
+    if (st0 + s0 < st1) issue(st0 + s0, s0);
+  int slot = 0;
+  for (int st = st0; st < st1; ++st) {
+    constexpr int AHEAD = R - 2;
+    if (st + AHEAD <= st1 - 1) wait_vmcnt<AHEAD * PER>();
+    else wait_vmcnt<0>();
+    const uint8_t* sl = ring + slot * SLOT;
+    u32x4 bq[2][4], wr[NT][2];
+#pragma unroll
+    for (int gi = 0; gi < 2; ++gi)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        bq[gi][j] = lds128(sl + T_OFF + trow * 512 + 16 * ((16 * gi + 4 * g4 + j) ^ tok_swz(trow)));
+#pragma unroll
+    for (int s2 = 0; s2 < NT; ++s2)
+#pragma unroll
+      for (int gi = 0; gi < 2; ++gi)
+        wr[s2][gi] = lds128(sl + s2 * 2048 + r16 * 128 + 16 * ((4 * gi + g4) ^ lds_swz(r16)));
+    // Scale and zero-point terms of the lane's four result rows 4*g4 + i.
+    uint32_t sw[NT][4], zw[NT][4];
+#pragma unroll
+    for (int s2 = 0; s2 < NT; ++s2)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int n = 4 * g4 + i;
+        sw[s2][i] = *reinterpret_cast<const uint32_t*>(sl + S_OFF + 4 * (16 * s2 + n));
+        zw[s2][i] = ZP ? *reinterpret_cast<const uint32_t*>(sl + S_OFF + 4 * (32 + 8 * s2 + (n >> 1))) : 0u;
+      }
+    // The consumed slot of the last step is free: every read of it is done.
+    const int next = st + R - 1;
+    if (next < st1) issue(next, slot == 0 ? R - 1 : slot - 1);
+#pragma unroll
+    for (int gi = 0; gi < 2; ++gi) {
+      v4f asum = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if constexpr (F16) asum = mfma_f16(__builtin_bit_cast(f16x8, ones), __builtin_bit_cast(f16x8, bq[gi][j]), asum);
+        else asum = mfma_bf16(__builtin_bit_cast(bf16x8, ones), __builtin_bit_cast(bf16x8, bq[gi][j]), asum);
+      }
+#pragma unroll
+      for (int s2 = 0; s2 < NT; ++s2) {
+        v4f part = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t d = wr[s2][gi][j];
+          const uint32_t lo = d & 0x0f0f0f0fu, hi = (d >> 4) & 0x0f0f0f0fu;
+          const uint32_t x0 = __builtin_amdgcn_perm(hi, lo, 0x05010400u);  // codes of k 0..3
+          const uint32_t x1 = __builtin_amdgcn_perm(hi, lo, 0x07030602u);  // codes of k 4..7
+          u32x4 wq;
+          wq[0] = __builtin_amdgcn_perm(HI, x0, 0x04010400u);
+          wq[1] = __builtin_amdgcn_perm(HI, x0, 0x04030402u);
+          wq[2] = __builtin_amdgcn_perm(HI, x1, 0x04010400u);
+          wq[3] = __builtin_amdgcn_perm(HI, x1, 0x04030402u);
+          if constexpr (F16) part = mfma_f16(__builtin_bit_cast(f16x8, wq), __builtin_bit_cast(f16x8, bq[gi][j]), part);
+          else part = mfma_bf16(__builtin_bit_cast(bf16x8, wq), __builtin_bit_cast(bf16x8, bq[gi][j]), part);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int n = 4 * g4 + i;
+          const float sc = sval((sw[s2][i] >> (16 * gi)) & 0xffffu);
+          float z = 8.0f;
+          if constexpr (ZP) {
+            const int zr = min(wrow0[s2] + 2 * (n >> 1), p.N - 2);
+            const uintptr_t za = reinterpret_cast<uintptr_t>(p.wz) +
+                                 (uintptr_t)(wzero_row(p, expert, zr) + (int64_t)(2 * st + gi) * p.wz_ks);
+            const uint32_t zb = (zw[s2][i] >> (8u * (uint32_t)(za & 3u))) & 0xffu;
+            z = (float)((n & 1) ? (zb >> 4) : (zb & 15u));
+          }
+          acc[s2][i] = fmaf(-(OFF + z) * sc, asum[i], fmaf(sc, part[i], acc[s2][i]));
+        }
+      }
+    }
+    slot = slot == R - 1 ? 0 : slot + 1;
+  }
+
+  if constexpr (KS > 1) {
+    wait_vmcnt<0>();
+    float* red = reinterpret_cast<float*>(ring);
+#pragma unroll
+    for (int s2 = 0; s2 < NT; ++s2)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) red[(s2 * 4 + i) * 64 + lane] = acc[s2][i];
+    __syncthreads();
+    if (kw != 0) return;
+#pragma unroll
+    for (int w = 1; w < KS; ++w) {
+      const float* rw = reinterpret_cast<const float*>(ring_all + w * (R * SLOT));
+#pragma unroll
+      for (int s2 = 0; s2 < NT; ++s2)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[s2][i] += rw[(s2 * 4 + i) * 64 + lane];
+    }
+  }
+  if (nout0 >= p.n_out) return;
+  int brow, orow;
+  bool bval;
+  token_row<true>(p, m0 + r16, brow, orow, bval);
+  if (!bval) return;
+#pragma unroll
+  for (int so = 0; so < NTH; ++so) {
+    float g[4], u[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      g[i] = acc[so][i];
+      u[i] = GATED ? acc[1][i] : 0.f;
+    }
+    finish_float4<EPI, ACT, true>(p, orow, nout0 + 16 * so + 4 * g4, g, u);
+  }
 }
 
 // ============================================================ tiled16
@@ -1100,11 +1341,71 @@ int launch_tiled16(const G16& p, int grid_y_moe, hipStream_t st, const char* op)
   return launch_tiled16_as<FMT, BM, BN, WM, WN, NP, MOE, EPI, ACT, F16, false>(p, grid_y_moe, st, op);
 }
 
+// ring16 takes int4 experts with bf16/fp16 scales per 128-K group (and zero
+// points) laid out so that each step's two scale elements of a row, and the
+// two zero-point bytes of a row pair, sit in one aligned 4-byte word; K a
+// multiple of 256 and 16-byte aligned weight and token rows.
+template <int FMT>
+bool ring16_ok(const G16& p, int64_t a_rows) {
+  if constexpr (FMT != kWInt4Zp && FMT != kWInt4Sym) return false;
+  else {
+    auto al = [](const void* q, uintptr_t a) { return (reinterpret_cast<uintptr_t>(q) % a) == 0; };
+    bool ok = p.K % 256 == 0 && p.ws_kgroup == 128 && (p.ws_kind == kSBf16 || p.ws_kind == kSF16) &&
+              p.ws_ks == 1 && p.ws_nblock == 1 && p.ws_ns % 2 == 0 && p.ws_es % 2 == 0 && al(p.ws, 4) &&
+              p.ldw % 16 == 0 && p.w_es % 16 == 0 && al(p.w, 16) && (p.lda * 2) % 16 == 0 && al(p.a, 16) &&
+              p.gate_off % 2 == 0 && p.N % 2 == 0 && (uint64_t)p.N * (uint64_t)p.ldw < (1ull << 32) &&
+              (uint64_t)a_rows * (uint64_t)(p.lda * 2) < (1ull << 32);
+    if (FMT == kWInt4Zp)
+      ok = ok && p.wz_ks == 1 && p.wz_ns % 2 == 0 && p.wz_es % 2 == 0 && al(p.wz, 4);
+    return ok;
+  }
+}
+
+// Token rows per slot: a block holds at most min(16, tokens) routed rows
+// (an expert takes each token once), and its routed rows come first.
+template <int FMT, int EPI, int ACT, bool F16>
+int launch_ring16(const G16& p, int num_blocks, hipStream_t st, const char* op) {
+  constexpr int NTH = (EPI == kEpiGated) ? 1 : 2;
+  const int grid_x = (p.n_out + 16 * NTH - 1) / (16 * NTH);
+  const int64_t tokens = (p.num_slots + p.top_k - 1) / p.top_k;
+  const int tq = tokens <= 2 ? 2 : (tokens <= 8 ? 8 : 16);
+  const int64_t live = std::min<int64_t>(num_blocks, p.num_slots);
+  const int steps = p.K / 256;
+  // K-split waves: the most of 1..4 that leaves every wave a step and stays
+  // within about six waves per CU.
+  int ks = 1;
+  for (int c : {2, 3, 4})
+    if (c <= steps && (int64_t)grid_x * live * c <= 6 * cu_count()) ks = c;
+  auto go = [&](auto tq_tag, auto ks_tag) {
+    constexpr int TQ_ = decltype(tq_tag)::value;
+    constexpr int KS_ = decltype(ks_tag)::value;
+    hipLaunchKernelGGL((ring16_kernel<FMT, TQ_, KS_, 3, EPI, ACT, F16>), dim3(grid_x, num_blocks), dim3(64 * KS_), 0,
+                       st, p);
+  };
+  auto with_ks = [&](auto tq_tag) {
+    if (ks == 4) go(tq_tag, std::integral_constant<int, 4>{});
+    else if (ks == 3) go(tq_tag, std::integral_constant<int, 3>{});
+    else if (ks == 2) go(tq_tag, std::integral_constant<int, 2>{});
+    else go(tq_tag, std::integral_constant<int, 1>{});
+  };
+  if (tq == 2) with_ks(std::integral_constant<int, 2>{});
+  else if (tq == 8) with_ks(std::integral_constant<int, 8>{});
+  else with_ks(std::integral_constant<int, 16>{});
+  return check_launch(op);
+}
+
 template <int FMT, int EPI, int ACT, bool F16>
 int moe16_dispatch(const G16& p, int block_m, int num_blocks, hipStream_t st, const char* op) {
   constexpr int NTS = (EPI == kEpiGated) ? 2 : 1;
   switch (block_m) {
     case 16: {
+      // int4 with K of at least four 256-K steps: the LDS ring (C5's w13 at
+      // T=1 11.3 -> 7.9 us). Shorter K stays on stream16 (C5's w2, K=768:
+      // 5.8 us there against 7.0-7.5 on the ring).
+      if constexpr (FMT == kWInt4Zp || FMT == kWInt4Sym) {
+        if (p.ring16 && p.K >= 1024 && ring16_ok<FMT>(p, p.a_rows))
+          return launch_ring16<FMT, EPI, ACT, F16>(p, num_blocks, st, op);
+      }
       // Four K-split waves, or two when K holds fewer than 12 chunks (a
       // fourth wave would get none): C5's w2 (K=768, six chunks) 8.8 -> 7.0
       // us at T=1, 25.2 -> 20.6 us at T=8; longer K is faster with four
@@ -1183,6 +1484,7 @@ int run_moe16(const char* op, const MoeArgs& m, G16 p, void* stream) {
   p.M = (int)m.num_slots; p.N = (int)m.N; p.K = (int)m.K; p.n_out = (int)n_out; p.gate_off = (int)(m.N / 2);
   p.sorted_ids = m.sorted_ids; p.sorted_len = m.sorted_len; p.expert_ids = m.expert_ids; p.num_post = m.num_post;
   p.num_slots = (int)m.num_slots; p.top_k = (int)m.top_k; p.topk_w = m.topk_w;
+  p.a_rows = m.num_slots; p.ring16 = 1;
   hipStream_t st = as_stream(stream);
   const int nb = (int)m.num_blocks, bm = (int)m.block_m;
   const bool f16 = m.a_dtype == STRIX_F16;

@@ -59,6 +59,32 @@ def test_zp_expert_gemm(tokens, block_m, gemm, activation, zp_experts):
     assert peak_rel_err(c, _ref(a, deq, ids, a_topk, weights, gemm, activation, cols)) <= TOL
 
 
+@pytest.mark.parametrize("tokens", [1, 5, 40])
+@pytest.mark.parametrize("gemm", ["w13", "w2"])
+def test_zp_expert_gemm_fp16_activations(tokens, gemm, zp_experts):
+    """fp16 tokens and output through the decode paths (block_m 16), whose
+    folded int4 decode feeds the codes to the fp16 MFMA as 1024 + q."""
+    d = zp_experts
+    g = torch.Generator().manual_seed(tokens + 991)
+    ids = torch.stack([torch.randperm(E, generator=g)[:TOPK] for _ in range(tokens)]).to(torch.int32)
+    w, s, z = d[gemm], d[gemm + "_s"], d[gemm + "_z"]
+    n, k = w.size(1), w.size(2) * 8
+    if gemm == "w13":
+        a = torch.randn(tokens, k, generator=g).to(torch.float16)
+        a_topk, weights, cols = TOPK, None, n // 2
+    else:
+        a = torch.randn(tokens * TOPK, k, generator=g).to(torch.float16)
+        a_topk, weights, cols = 1, torch.rand(tokens, TOPK, generator=g), n
+    sorted_ids, expert_ids, num_post = torch.ops.strix.moe_align(ids.to(DEV), E, 16)
+    c = torch.full((tokens * TOPK, cols), float("nan"), dtype=torch.float16, device=DEV)
+    torch.ops.strix.moe_gemm_w4a16_zp(c, a.to(DEV), w.to(DEV), s.to(DEV), z.to(DEV), sorted_ids, expert_ids, num_post,
+                                      None if weights is None else weights.reshape(-1).to(DEV), a_topk, 16, 64,
+                                      gemm == "w13", "silu", 128)
+    deq = oracle.wna16_zp_decode(w, s, z, 128)
+    assert not torch.isnan(c).any()
+    assert peak_rel_err(c, _ref(a, deq, ids, a_topk, weights, gemm, "silu", cols)) <= TOL
+
+
 # Reference shapes: tests/test_moe_wna16.py:14-20 (gemma group 32, qfn group 128).
 @pytest.mark.parametrize("model", [(32, 8, 32, (1408, 2816), (2816, 704)), (16, 10, 128, (1280, 2560), (2560, 640))])
 @pytest.mark.parametrize("tokens", [1, 5, 70])
