@@ -900,6 +900,25 @@ __global__ void __launch_bounds__((WM * WN + NP) * 64) tiled16_kernel(G16 p, int
     dense_tile(blockIdx.x, tiles_m, tiles_n, group_m, tm, tn);
   }
   const int m0 = tm * BM;
+  // MoE: a consumer wave runs the MFMAs of its 16-row token subtiles up to
+  // the last one that holds a routed row (an expert's last row tile is
+  // mostly padding), and none when all its rows are padding; it still takes
+  // part in every copy, decode and barrier.
+  int mt_live = MT;
+  if constexpr (MOE) {
+    int hi = -1;   // highest routed row of the wave's TM rows
+#pragma unroll
+    for (int j = 0; j < (TM + 63) / 64; ++j) {
+      const int r = 64 * j + lane;
+      int br, orw;
+      bool v;
+      token_row<true>(p, m0 + wm * TM + r, br, orw, v);
+      const uint64_t mask = __ballot(v && r < TM);
+      if (mask) hi = 64 * j + 63 - __builtin_clzll(mask);
+    }
+    mt_live = (hi + 16) / 16;
+  }
+  const bool do_mma = is_cons && mt_live > 0;
   auto wrow_of = [&](int r) -> int {  // weight row of LDS weight row r (0..BN-1)
     if constexpr (GATED) {
       const int base = tn * (BN / 2);
@@ -1126,8 +1145,10 @@ __global__ void __launch_bounds__((WM * WN + NP) * 64) tiled16_kernel(G16 p, int
 #pragma unroll
           for (int s = 0; s < NT; ++s) af1[s] = lds128(st + aidx[s] * 2048 + frag1);
         }
+        if (!MOE || t < mt_live) {
 #pragma unroll
-        for (int s = 0; s < NT; ++s) mma(step ? af1[s] : af0[s], bq[t % 3], acc[s][t]);
+          for (int s = 0; s < NT; ++s) mma(step ? af1[s] : af0[s], bq[t % 3], acc[s][t]);
+        }
         // One scheduling region per token row: the read two rows ahead goes
         // out before this row's MFMAs, so each fragment has about seven MFMAs
         // of cover before its use (the compiler's own order waited on every
@@ -1162,7 +1183,7 @@ __global__ void __launch_bounds__((WM * WN + NP) * 64) tiled16_kernel(G16 p, int
         dma_raw(clampk(kb + 3), (kb + 3) % 3);
         copy_a(clampk(kb + 2), (kb + 2) % STAGES);
       }
-      if (is_cons) compute(kb);
+      if (do_mma) compute(kb);
     }
   }
   auto body = [&](int kb, WBuf& wdec) {
@@ -1176,7 +1197,7 @@ __global__ void __launch_bounds__((WM * WN + NP) * 64) tiled16_kernel(G16 p, int
       load_w(clampk(kb + 3), wdec);
       copy_a(clampk(kb + 2), (kb + 2) % STAGES);
     }
-    if (is_cons) compute(kb);
+    if (do_mma) compute(kb);
   };
   if constexpr (!RAWL) {
     WBuf wA, wB;  // raw weights of even / odd stages

@@ -701,6 +701,20 @@ __global__ void __launch_bounds__(WM * WN * 64) tiled8_kernel(G8 p, int tiles_m,
     dense_tile(blockIdx.x, tiles_m, tiles_n, group_m, tm, tn);
   }
   const int m0 = tm * BM;
+  // MoE: a wave whose TM token rows are all padding (in an expert's last,
+  // partly filled row tile) skips its fragment reads, MFMAs and folds; it
+  // still issues its copies and takes every barrier.
+  bool rows_live = true;
+  if constexpr (MOE) {
+    bool any = false;
+    for (int r = lane; r < TM; r += 64) {
+      int br, orw;
+      bool v;
+      token_row<true>(p, m0 + wm * TM + r, br, orw, v);
+      any = any || v;
+    }
+    rows_live = __ballot(any) != 0;
+  }
   auto wrow_of = [&](int j) -> int {  // first weight row of LDS weight subtile j
     if constexpr (GATED) {
       const int base = tn * (BN / 2);
@@ -841,127 +855,129 @@ __global__ void __launch_bounds__(WM * WN * 64) tiled8_kernel(G8 p, int tiles_m,
     lds_barrier();
     if (kb + STAGES - 1 < nkb) issue(kb + STAGES - 1, (kb + STAGES - 1) % STAGES);
 
-    const uint8_t* st = smem + buf * STAGE;
-    v8i bf[MT];
-#pragma unroll
-    for (int t = 0; t < MT; ++t) {
-      const uint8_t* sub = st + TOK_BASE + (wm * MT + t) * 2048;
-      bf[t] = cat8(lds128(sub + frag0), lds128(sub + frag1));
-    }
-    float sa_t[MT];
-    if constexpr (HAS_SA) {
-      const float* sl = reinterpret_cast<const float*>(st + SA_OFF);
-#pragma unroll
-      for (int t = 0; t < MT; ++t) sa_t[t] = sl[wm * TM + 16 * t + r16];
-    }
-    const float* swl = reinterpret_cast<const float*>(st + SW_OFF);
-    float c1[MT];
-    if constexpr (KIND == kFp8Block && ONE_SW) {
-      const float sw = swl[aidx[0]];
-#pragma unroll
-      for (int t = 0; t < MT; ++t) c1[t] = sw * sa_t[t];
-    }
-    auto afrag = [&](int s) -> v8i {
-      if constexpr (W4) {
-        // Lane (r16, g4) needs k 16*g4 + [0,16) of each 64-K half: 8 packed
-        // bytes at 32*h + 8*g4, i.e. chunk 2h + g4/2 at offset 8*(g4 & 1).
-        const uint8_t* row = st + aidx[s] * 1024 + r16 * 64 + 8 * (g4 & 1);
-        const int sw4 = (r16 >> 2) & 3;
-        const uint2 h0 = *reinterpret_cast<const uint2*>(row + 16 * ((g4 >> 1) ^ sw4));
-        const uint2 h1 = *reinterpret_cast<const uint2*>(row + 16 * ((2 + (g4 >> 1)) ^ sw4));
-        return widen_int4<W4>(h0, h1);
-      } else {
-        const uint8_t* sub = st + aidx[s] * 2048;
-        return cat8(lds128(sub + frag0), lds128(sub + frag1));
-      }
-    };
-    // Software pipeline over the weight subtiles: the fragment of subtile
-    // s+1 is read while subtile s runs its MFMAs, and the block-scale fold
-    // of subtile s-1 is issued between them, so no fold waits on the MFMA
-    // that produced its operand. sched_barrier keeps each step's
-    // instructions in that step; the group barriers interleave one MFMA with
-    // the fold of one earlier result.
-    v8i afc = afrag(0);
-#pragma unroll
-    for (int s = 0; s < NT; ++s) {
-      v8i afn;
-      if (s + 1 < NT) afn = afrag(s + 1);
-      v8i af = afc;
-      if constexpr (WX128) af = flip80(af);
-      v4f part_f[MT];
-      v4i part_i[MT];
-      float cur_sw[4];
-      if constexpr (KIND == kFp8Block) {
-        cur_sw[0] = ONE_SW ? 0.f : swl[aidx[s]];
-#pragma unroll
-        for (int t = 0; t < MT; ++t) part_f[t] = mfma_fp8(af, bf[t], v4f{0.f, 0.f, 0.f, 0.f});
-      } else if constexpr (KIND == kI8Token) {
-#pragma unroll
-        for (int t = 0; t < MT; ++t) {
-          acci[s][t] = mfma_i8(lo4(af), lo4(bf[t]), acci[s][t]);
-          acci[s][t] = mfma_i8(hi4(af), hi4(bf[t]), acci[s][t]);
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) cur_sw[i] = swl[16 * aidx[s] + 4 * g4 + i];
-#pragma unroll
-        for (int t = 0; t < MT; ++t) {
-          part_i[t] = mfma_i8(lo4(af), lo4(bf[t]), v4i{0, 0, 0, 0});
-          part_i[t] = mfma_i8(hi4(af), hi4(bf[t]), part_i[t]);
-        }
-      }
-      // The fold's scale of subtile s' and token subtile t, row i of the lane's four.
-      auto fold_c = [&](const float* sw, int t, int i) -> float {
-        if constexpr (KIND == kFp8Block) return ONE_SW ? c1[t] : sw[0] * sa_t[t];
-        else return sw[i] * sa_t[t];
-      };
-      if constexpr (!INT_ACC) {
-        if (s > 0) {
-#pragma unroll
-          for (int t = 0; t < MT; ++t)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const float v = (KIND == kFp8Block) ? prev_f[t][i] : (float)prev_i[t][i] * kW4Unit<W4>;
-              acc[s - 1][t][i] = fmaf(v, fold_c(prev_sw, t, i), acc[s - 1][t][i]);
-            }
-        } else {
-#pragma unroll
-          for (int t = 0; t < MT; ++t)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const float v = (KIND == kFp8Block) ? prev_f[t][i] : (float)prev_i[t][i] * kW4Unit<W4>;
-              const float c = (KIND == kFp8Block) ? (ONE_SW ? prev_c1[t] : prev_sw[0] * prev_sa[t])
-                                                  : prev_sw[i] * prev_sa[t];
-              acc[NT - 1][t][i] = fmaf(v, c, acc[NT - 1][t][i]);
-            }
-        }
-#pragma unroll
-        for (int t = 0; t < MT; ++t) {
-          prev_f[t] = part_f[t];
-          prev_i[t] = part_i[t];
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) prev_sw[i] = cur_sw[i];
-        // The next fragment's reads go out after this subtile's first MFMA:
-        // the wait for them then comes one subtile later, never right after
-        // they are issued.
-#pragma unroll
-        for (int t = 0; t < MT; ++t) {
-          __builtin_amdgcn_sched_group_barrier(0x008, KIND == kFp8Block ? 1 : 2, 0);
-          if (t == 0 && s + 1 < NT) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-          __builtin_amdgcn_sched_group_barrier(0x002, KIND == kFp8Block ? 4 : 8, 0);
-        }
-      }
-      if (s + 1 < NT) afc = afn;
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    if constexpr (!INT_ACC) {
+    if (rows_live) {  // the K block's fragment reads, MFMAs and folds
+      const uint8_t* st = smem + buf * STAGE;
+      v8i bf[MT];
 #pragma unroll
       for (int t = 0; t < MT; ++t) {
-        prev_sa[t] = sa_t[t];
-        if constexpr (KIND == kFp8Block && ONE_SW) prev_c1[t] = c1[t];
+        const uint8_t* sub = st + TOK_BASE + (wm * MT + t) * 2048;
+        bf[t] = cat8(lds128(sub + frag0), lds128(sub + frag1));
       }
-    }
+      float sa_t[MT];
+      if constexpr (HAS_SA) {
+        const float* sl = reinterpret_cast<const float*>(st + SA_OFF);
+#pragma unroll
+        for (int t = 0; t < MT; ++t) sa_t[t] = sl[wm * TM + 16 * t + r16];
+      }
+      const float* swl = reinterpret_cast<const float*>(st + SW_OFF);
+      float c1[MT];
+      if constexpr (KIND == kFp8Block && ONE_SW) {
+        const float sw = swl[aidx[0]];
+#pragma unroll
+        for (int t = 0; t < MT; ++t) c1[t] = sw * sa_t[t];
+      }
+      auto afrag = [&](int s) -> v8i {
+        if constexpr (W4) {
+          // Lane (r16, g4) needs k 16*g4 + [0,16) of each 64-K half: 8 packed
+          // bytes at 32*h + 8*g4, i.e. chunk 2h + g4/2 at offset 8*(g4 & 1).
+          const uint8_t* row = st + aidx[s] * 1024 + r16 * 64 + 8 * (g4 & 1);
+          const int sw4 = (r16 >> 2) & 3;
+          const uint2 h0 = *reinterpret_cast<const uint2*>(row + 16 * ((g4 >> 1) ^ sw4));
+          const uint2 h1 = *reinterpret_cast<const uint2*>(row + 16 * ((2 + (g4 >> 1)) ^ sw4));
+          return widen_int4<W4>(h0, h1);
+        } else {
+          const uint8_t* sub = st + aidx[s] * 2048;
+          return cat8(lds128(sub + frag0), lds128(sub + frag1));
+        }
+      };
+      // Software pipeline over the weight subtiles: the fragment of subtile
+      // s+1 is read while subtile s runs its MFMAs, and the block-scale fold
+      // of subtile s-1 is issued between them, so no fold waits on the MFMA
+      // that produced its operand. sched_barrier keeps each step's
+      // instructions in that step; the group barriers interleave one MFMA with
+      // the fold of one earlier result.
+      v8i afc = afrag(0);
+#pragma unroll
+      for (int s = 0; s < NT; ++s) {
+        v8i afn;
+        if (s + 1 < NT) afn = afrag(s + 1);
+        v8i af = afc;
+        if constexpr (WX128) af = flip80(af);
+        v4f part_f[MT];
+        v4i part_i[MT];
+        float cur_sw[4];
+        if constexpr (KIND == kFp8Block) {
+          cur_sw[0] = ONE_SW ? 0.f : swl[aidx[s]];
+#pragma unroll
+          for (int t = 0; t < MT; ++t) part_f[t] = mfma_fp8(af, bf[t], v4f{0.f, 0.f, 0.f, 0.f});
+        } else if constexpr (KIND == kI8Token) {
+#pragma unroll
+          for (int t = 0; t < MT; ++t) {
+            acci[s][t] = mfma_i8(lo4(af), lo4(bf[t]), acci[s][t]);
+            acci[s][t] = mfma_i8(hi4(af), hi4(bf[t]), acci[s][t]);
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) cur_sw[i] = swl[16 * aidx[s] + 4 * g4 + i];
+#pragma unroll
+          for (int t = 0; t < MT; ++t) {
+            part_i[t] = mfma_i8(lo4(af), lo4(bf[t]), v4i{0, 0, 0, 0});
+            part_i[t] = mfma_i8(hi4(af), hi4(bf[t]), part_i[t]);
+          }
+        }
+        // The fold's scale of subtile s' and token subtile t, row i of the lane's four.
+        auto fold_c = [&](const float* sw, int t, int i) -> float {
+          if constexpr (KIND == kFp8Block) return ONE_SW ? c1[t] : sw[0] * sa_t[t];
+          else return sw[i] * sa_t[t];
+        };
+        if constexpr (!INT_ACC) {
+          if (s > 0) {
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                const float v = (KIND == kFp8Block) ? prev_f[t][i] : (float)prev_i[t][i] * kW4Unit<W4>;
+                acc[s - 1][t][i] = fmaf(v, fold_c(prev_sw, t, i), acc[s - 1][t][i]);
+              }
+          } else {
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                const float v = (KIND == kFp8Block) ? prev_f[t][i] : (float)prev_i[t][i] * kW4Unit<W4>;
+                const float c = (KIND == kFp8Block) ? (ONE_SW ? prev_c1[t] : prev_sw[0] * prev_sa[t])
+                                                    : prev_sw[i] * prev_sa[t];
+                acc[NT - 1][t][i] = fmaf(v, c, acc[NT - 1][t][i]);
+              }
+          }
+#pragma unroll
+          for (int t = 0; t < MT; ++t) {
+            prev_f[t] = part_f[t];
+            prev_i[t] = part_i[t];
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i) prev_sw[i] = cur_sw[i];
+          // The next fragment's reads go out after this subtile's first MFMA:
+          // the wait for them then comes one subtile later, never right after
+          // they are issued.
+#pragma unroll
+          for (int t = 0; t < MT; ++t) {
+            __builtin_amdgcn_sched_group_barrier(0x008, KIND == kFp8Block ? 1 : 2, 0);
+            if (t == 0 && s + 1 < NT) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, KIND == kFp8Block ? 4 : 8, 0);
+          }
+        }
+        if (s + 1 < NT) afc = afn;
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if constexpr (!INT_ACC) {
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          prev_sa[t] = sa_t[t];
+          if constexpr (KIND == kFp8Block && ONE_SW) prev_c1[t] = c1[t];
+        }
+      }
+    }  // rows_live
   }
   if constexpr (!INT_ACC) {
 #pragma unroll
