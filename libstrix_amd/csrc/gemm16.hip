@@ -919,6 +919,16 @@ __global__ void __launch_bounds__((WM * WN + NP) * 64) tiled16_kernel(G16 p, int
     mt_live = (hi + 16) / 16;
   }
   const bool do_mma = is_cons && mt_live > 0;
+  // MoE epilogue rows, loaded before the K loop (dense rows are arithmetic;
+  // the register-staged raw-weight path has no registers to spare for them).
+  constexpr bool PRE = MOE && RAWL;
+  EpiRow erow[PRE ? MT : 1];
+  if constexpr (PRE) {
+    if (is_cons) {
+#pragma unroll
+      for (int t = 0; t < MT; ++t) erow[t] = epi_row<MOE>(p, m0 + wm * TM + 16 * t + r16);
+    }
+  }
   auto wrow_of = [&](int r) -> int {  // weight row of LDS weight row r (0..BN-1)
     if constexpr (GATED) {
       const int base = tn * (BN / 2);
@@ -1223,10 +1233,9 @@ __global__ void __launch_bounds__((WM * WN + NP) * 64) tiled16_kernel(G16 p, int
 
 #pragma unroll
   for (int t = 0; t < MT; ++t) {
-    int br, orw;
-    bool v;
-    token_row<MOE>(p, m0 + wm * TM + 16 * t + r16, br, orw, v);
-    if (!v) continue;
+    const EpiRow e = PRE ? erow[PRE ? t : 0] : epi_row<MOE>(p, m0 + wm * TM + 16 * t + r16);
+    const int orw = e.orow;
+    if (!e.valid) continue;
 #pragma unroll
     for (int so = 0; so < NTH; ++so) {
       float g[4], u[4];
@@ -1246,7 +1255,7 @@ __global__ void __launch_bounds__((WM * WN + NP) * 64) tiled16_kernel(G16 p, int
             }
         }
       }
-      finish_float4<EPI, ACT, MOE>(p, orw, col0, g, u);
+      finish_float4_tw<EPI, ACT, MOE>(p, orw, col0, g, u, e.tw);
     }
   }
 }

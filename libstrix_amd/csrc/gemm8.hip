@@ -67,8 +67,8 @@ __device__ __forceinline__ v8i flip80(const v8i& x) {
 // up values when gated. I8 token values arrive as int32 bit patterns and are
 // scaled here: (acc * sa[m]) * sw[n].
 template <int KIND, int EPI, int ACT, bool MOE>
-__device__ __forceinline__ void finish4(const G8& p, int orow, int brow, bool valid, int col0,
-                                        const float g[4], const float u[4]) {
+__device__ __forceinline__ void finish4_tw(const G8& p, int orow, int brow, bool valid, int col0,
+                                           const float g[4], const float u[4], float tw) {
   if (!valid) return;
   if constexpr (EPI == kEpiI32) {
     int iv[4];
@@ -85,10 +85,16 @@ __device__ __forceinline__ void finish4(const G8& p, int orow, int brow, bool va
       const int n = min(col0 + i, p.N - 1);
       v[i] = ((float)__float_as_int(g[i]) * sa) * p.sw[(int64_t)n * p.sw_ns];
     }
-    finish_float4<kEpiStore, ACT, MOE>(p, orow, col0, v, u);
+    finish_float4_tw<kEpiStore, ACT, MOE>(p, orow, col0, v, u, tw);
   } else {
-    finish_float4<EPI, ACT, MOE>(p, orow, col0, g, u);
+    finish_float4_tw<EPI, ACT, MOE>(p, orow, col0, g, u, tw);
   }
+}
+template <int KIND, int EPI, int ACT, bool MOE>
+__device__ __forceinline__ void finish4(const G8& p, int orow, int brow, bool valid, int col0,
+                                        const float g[4], const float u[4]) {
+  const float tw = (MOE && valid && p.topk_w) ? p.topk_w[orow] : 1.f;
+  finish4_tw<KIND, EPI, ACT, MOE>(p, orow, brow, valid, col0, g, u, tw);
 }
 
 // ============================================================ stream8
@@ -715,6 +721,12 @@ __global__ void __launch_bounds__(WM * WN * 64) tiled8_kernel(G8 p, int tiles_m,
     }
     rows_live = __ballot(any) != 0;
   }
+  // MoE epilogue rows, loaded before the K loop (dense rows are arithmetic).
+  EpiRow erow[MOE ? MT : 1];
+  if constexpr (MOE) {
+#pragma unroll
+    for (int t = 0; t < MT; ++t) erow[t] = epi_row<MOE>(p, m0 + wm * TM + 16 * t + r16);
+  }
   auto wrow_of = [&](int j) -> int {  // first weight row of LDS weight subtile j
     if constexpr (GATED) {
       const int base = tn * (BN / 2);
@@ -993,9 +1005,9 @@ __global__ void __launch_bounds__(WM * WN * 64) tiled8_kernel(G8 p, int tiles_m,
   // Epilogue straight from registers.
 #pragma unroll
   for (int t = 0; t < MT; ++t) {
-    int br, orw;
-    bool v;
-    token_row<MOE>(p, m0 + wm * TM + 16 * t + r16, br, orw, v);
+    const EpiRow e = MOE ? erow[MOE ? t : 0] : epi_row<MOE>(p, m0 + wm * TM + 16 * t + r16);
+    const int br = e.brow, orw = e.orow;
+    const bool v = e.valid;
 #pragma unroll
     for (int so = 0; so < NTH; ++so) {
       float g[4], u[4];
@@ -1007,7 +1019,7 @@ __global__ void __launch_bounds__(WM * WN * 64) tiled8_kernel(G8 p, int tiles_m,
       }
       const int col0 = GATED ? (tn * (BN / 2) + 16 * (wn * NTH + so) + 4 * g4)
                              : (tn * BN + 16 * (wn * NT + so) + 4 * g4);
-      finish4<KIND, EPI, ACT, MOE>(p, orw, br, v, col0, g, u);
+      finish4_tw<KIND, EPI, ACT, MOE>(p, orw, br, v, col0, g, u, e.tw);
     }
   }
 }

@@ -93,7 +93,8 @@ __device__ __forceinline__ void store4_i32(const P& p, int orow, int col0, const
 // Float epilogue of one lane's four results: act(g)*u when gated, times the
 // slot's top-k weight (MoE, when given), then the store.
 template <int EPI, int ACT, bool MOE, class P>
-__device__ __forceinline__ void finish_float4(const P& p, int orow, int col0, const float g[4], const float u[4]) {
+__device__ __forceinline__ void finish_float4_tw(const P& p, int orow, int col0, const float g[4], const float u[4],
+                                                 float tw) {
   float v[4];
   if constexpr (EPI == kEpiGated) {
 #pragma unroll
@@ -104,12 +105,38 @@ __device__ __forceinline__ void finish_float4(const P& p, int orow, int col0, co
   }
   if constexpr (MOE) {
     if (p.topk_w) {
-      const float tw = p.topk_w[orow];
 #pragma unroll
       for (int i = 0; i < 4; ++i) v[i] *= tw;
     }
   }
   store4(p, orow, col0, v);
+}
+template <int EPI, int ACT, bool MOE, class P>
+__device__ __forceinline__ void finish_float4(const P& p, int orow, int col0, const float g[4], const float u[4]) {
+  const float tw = (MOE && p.topk_w) ? p.topk_w[orow] : 1.f;
+  finish_float4_tw<EPI, ACT, MOE>(p, orow, col0, g, u, tw);
+}
+
+// An epilogue row of a tiled kernel (MFMA column m): output row, whether it
+// is stored, and its top-k weight (MoE with weights; else 1). The tiled
+// kernels load these before their K loop: loaded in the epilogue they would
+// come one 16-row subtile at a time behind the previous subtile's stores.
+struct EpiRow {
+  int brow, orow;
+  int valid;
+  float tw;
+};
+template <bool MOE, class P>
+__device__ __forceinline__ EpiRow epi_row(const P& p, int m) {
+  EpiRow e;
+  bool v;
+  token_row<MOE>(p, m, e.brow, e.orow, v);
+  e.valid = v;
+  e.tw = 1.f;
+  if constexpr (MOE) {
+    if (p.topk_w && v) e.tw = p.topk_w[e.orow];
+  }
+  return e;
 }
 
 // The hardware deals the blocks of a launch to the eight XCDs round robin
