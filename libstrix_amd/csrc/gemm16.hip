@@ -894,8 +894,9 @@ __global__ void __launch_bounds__((WM * WN + NP) * 64) tiled16_kernel(G16 p, int
   int tm, tn, expert = 0;
   if constexpr (MOE) {
     if (!moe_tile(*p.num_post, BM, tm, tn)) return;
+    // Checked after the token-row loads below are issued, so the two
+    // lookups share one memory round trip.
     expert = p.expert_ids[tm];
-    if (expert < 0) return;
   } else {
     dense_tile(blockIdx.x, tiles_m, tiles_n, group_m, tm, tn);
   }
@@ -937,7 +938,6 @@ __global__ void __launch_bounds__((WM * WN + NP) * 64) tiled16_kernel(G16 p, int
       return tn * BN + r;
     }
   };
-  const uint8_t* wbase = p.w + (int64_t)expert * p.w_es;
 
   // Direct copies (token rows, and bf16 weight rows): 8 rows x 128 B each.
   uint32_t qoff[CPW > 0 ? CPW : 1];
@@ -960,6 +960,10 @@ __global__ void __launch_bounds__((WM * WN + NP) * 64) tiled16_kernel(G16 p, int
     }
     qoff[j] += 16 * ((lane & 7) ^ lds_swz(row + (DIRECT_W ? 0 : BN)));
   }
+  if constexpr (MOE) {
+    if (expert < 0) return;
+  }
+  const uint8_t* wbase = p.w + (int64_t)expert * p.w_es;
   // Decoded weight pieces of this thread: (LDS row, piece index within the row).
   int prow[PPT > 0 ? PPT : 1], pidx[PPT > 0 ? PPT : 1], pgrow[PPT > 0 ? PPT : 1];
 #pragma unroll

@@ -701,8 +701,9 @@ __global__ void __launch_bounds__(WM * WN * 64) tiled8_kernel(G8 p, int tiles_m,
   int tm, tn, expert = 0;
   if constexpr (MOE) {
     if (!moe_tile(*p.num_post, BM, tm, tn)) return;
+    // Checked after the token-row loads below are issued, so the two
+    // lookups share one memory round trip.
     expert = p.expert_ids[tm];
-    if (expert < 0) return;
   } else {
     dense_tile(blockIdx.x, tiles_m, tiles_n, group_m, tm, tn);
   }
@@ -740,7 +741,6 @@ __global__ void __launch_bounds__(WM * WN * 64) tiled8_kernel(G8 p, int tiles_m,
   // Copy q moves 8 operand rows x 128 contiguous bytes (8 whole cache
   // lines): lane l takes row 8q + l/8 and stores to LDS slot l%8 the 16-byte
   // chunk (l%8) ^ swz(row) of that row.
-  const uint8_t* wbase = p.w + (int64_t)expert * p.w_es;
   uint32_t qoff[QPW];
   bool qis_w[QPW];
 #pragma unroll
@@ -769,6 +769,10 @@ __global__ void __launch_bounds__(WM * WN * 64) tiled8_kernel(G8 p, int tiles_m,
     // (saddr form), so no 64-bit per-lane address stays live across the loop.
     asm("" : "+v"(qoff[j]));
   }
+  if constexpr (MOE) {
+    if (expert < 0) return;
+  }
+  const uint8_t* wbase = p.w + (int64_t)expert * p.w_es;
   // Fragment reads: lane l reads row 16*subtile + l%16, chunks l/16 (half 0)
   // and 4 + l/16 (half 1), at their swizzled slots.
   const uint32_t frag0 = (uint32_t)r16 * 128 + 16 * ((g4) ^ lds_swz(r16));
