@@ -205,6 +205,24 @@ __device__ __forceinline__ void mxfp4_dword_cvt(uint32_t d, uint32_t b, uint32_t
   out[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, sc, 3));
 }
 
+// 8 int4 codes of d (nibble i = value i) with zero point z -> 4 dwords of
+// 16-bit pairs (q - z) * s, as decode_dword gives them, in about 3 VALU
+// operations per value instead of 4.5: zb holds 16 - z in each byte, so a
+// byte of (d & 0x0f0f0f0f) + zb is v = q - z + 16 (1..31, no carry between
+// bytes), which one byte-to-float conversion takes exactly; fma(v, s, c)
+// with c = -16 s (exact) is (v - 16) s = (q - z) s rounded once, the same
+// bits as the product. The caller keeps |s| <= 2^123 so that c is finite.
+template <bool F16>
+__device__ __forceinline__ void int4_dword_fma(uint32_t d, uint32_t zb, float s, float c, uint32_t* out) {
+  const uint32_t lo = (d & 0x0f0f0f0fu) + zb, hi = ((d >> 4) & 0x0f0f0f0fu) + zb;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float v0 = (float)((lo >> (8 * j)) & 0xffu);
+    const float v1 = (float)((hi >> (8 * j)) & 0xffu);
+    out[j] = pack2<F16>(__builtin_fmaf(v0, s, c), __builtin_fmaf(v1, s, c));
+  }
+}
+
 // Decodes one dword of packed weights (8 values for 4-bit formats, 4 for
 // 8-bit) into 16-bit values, appending to out[] as packed pairs.
 template <int FMT, bool F16>
@@ -297,8 +315,12 @@ __global__ void __launch_bounds__(WAVES * 64) stream16_kernel(G16 p) {
   const uint8_t* wbase = p.w + (int64_t)expert * p.w_es;
   int brow[MT], orow[MT];
   bool bval[MT];
+  {
+    int mrow[MT];
 #pragma unroll
-  for (int t = 0; t < MT; ++t) token_row<MOE>(p, m0 + 16 * t + r16, brow[t], orow[t], bval[t]);
+    for (int t = 0; t < MT; ++t) mrow[t] = m0 + 16 * t + r16;
+    token_rows<MOE, MT>(p, mrow, brow, orow, bval);
+  }
 
   const int nfull = p.K / CK;
   const bool tail = (p.K % CK) != 0;  // 4-bit only: a 64-K tail (K % 64 == 0 is required)
@@ -652,13 +674,17 @@ __global__ void __launch_bounds__(64 * KS) ring16_kernel(G16 p) {
   // Token copy c: rows 2c + lane/32, chunk (lane%32) ^ tok_swz(row) of the row's 512 bytes.
   const uint8_t* abase = reinterpret_cast<const uint8_t*>(p.a);
   uint32_t toff[TC];
+  {
+    int mrow[TC], br[TC], orw[TC];
+    bool v[TC];
 #pragma unroll
-  for (int c = 0; c < TC; ++c) {
-    const int row = 2 * c + (lane >> 5);
-    int br, orw;
-    bool v;
-    token_row<true>(p, m0 + row, br, orw, v);
-    toff[c] = (uint32_t)br * (uint32_t)(p.lda * 2) + 16u * (uint32_t)((lane & 31) ^ tok_swz(row));
+    for (int c = 0; c < TC; ++c) mrow[c] = m0 + 2 * c + (lane >> 5);
+    token_rows<true, TC>(p, mrow, br, orw, v);
+#pragma unroll
+    for (int c = 0; c < TC; ++c) {
+      const int row = 2 * c + (lane >> 5);
+      toff[c] = (uint32_t)br[c] * (uint32_t)(p.lda * 2) + 16u * (uint32_t)((lane & 31) ^ tok_swz(row));
+    }
   }
   // Scale / zero-point word of this lane (element index of the step-0 word).
   const int srow_l = min(wrow0[(lane >> 4) & 1] + r16, p.N - 1);  // lanes 0..31: subtile lane/16, row lane%16
@@ -901,35 +927,43 @@ __global__ void __launch_bounds__((WM * WN + NP) * 64) tiled16_kernel(G16 p, int
     dense_tile(blockIdx.x, tiles_m, tiles_n, group_m, tm, tn);
   }
   const int m0 = tm * BM;
+  // MoE epilogue rows, loaded before the K loop (dense rows are arithmetic;
+  // the register-staged raw-weight path has no registers to spare for them).
+  constexpr bool PRE = MOE && RAWL;
+  EpiRow erow[PRE ? MT : 1];
   // MoE: a consumer wave runs the MFMAs of its 16-row token subtiles up to
   // the last one that holds a routed row (an expert's last row tile is
   // mostly padding), and none when all its rows are padding; it still takes
   // part in every copy, decode and barrier.
   int mt_live = MT;
-  if constexpr (MOE) {
+  if constexpr (PRE) {
+    if (is_cons) {
+      int mrow[MT];
+#pragma unroll
+      for (int t = 0; t < MT; ++t) mrow[t] = m0 + wm * TM + 16 * t + r16;
+      epi_rows<MOE, MT>(p, mrow, erow);
+      int live = 0;
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
+        if (__ballot(erow[t].valid)) live = t + 1;
+      mt_live = live;
+    }
+  } else if constexpr (MOE) {
+    constexpr int NJ = (TM + 63) / 64;
+    int mrow[NJ], br[NJ], orw[NJ];
+    bool v[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) mrow[j] = m0 + wm * TM + 64 * j + lane;
+    token_rows<true, NJ>(p, mrow, br, orw, v);
     int hi = -1;   // highest routed row of the wave's TM rows
 #pragma unroll
-    for (int j = 0; j < (TM + 63) / 64; ++j) {
-      const int r = 64 * j + lane;
-      int br, orw;
-      bool v;
-      token_row<true>(p, m0 + wm * TM + r, br, orw, v);
-      const uint64_t mask = __ballot(v && r < TM);
+    for (int j = 0; j < NJ; ++j) {
+      const uint64_t mask = __ballot(v[j] && 64 * j + lane < TM);
       if (mask) hi = 64 * j + 63 - __builtin_clzll(mask);
     }
     mt_live = (hi + 16) / 16;
   }
   const bool do_mma = is_cons && mt_live > 0;
-  // MoE epilogue rows, loaded before the K loop (dense rows are arithmetic;
-  // the register-staged raw-weight path has no registers to spare for them).
-  constexpr bool PRE = MOE && RAWL;
-  EpiRow erow[PRE ? MT : 1];
-  if constexpr (PRE) {
-    if (is_cons) {
-#pragma unroll
-      for (int t = 0; t < MT; ++t) erow[t] = epi_row<MOE>(p, m0 + wm * TM + 16 * t + r16);
-    }
-  }
   auto wrow_of = [&](int r) -> int {  // weight row of LDS weight row r (0..BN-1)
     if constexpr (GATED) {
       const int base = tn * (BN / 2);
@@ -940,8 +974,20 @@ __global__ void __launch_bounds__((WM * WN + NP) * 64) tiled16_kernel(G16 p, int
   };
 
   // Direct copies (token rows, and bf16 weight rows): 8 rows x 128 B each.
-  uint32_t qoff[CPW > 0 ? CPW : 1];
-  bool qis_w[CPW > 0 ? CPW : 1];
+  constexpr int CPB = CPW > 0 ? CPW : 1;
+  uint32_t qoff[CPB];
+  bool qis_w[CPB];
+  int qbr[CPB];
+  {
+    int mrow[CPB], orw[CPB];
+    bool v[CPB];
+#pragma unroll
+    for (int j = 0; j < CPB; ++j) {
+      const int row = 8 * (pwave + PW * j) + (lane >> 3);
+      mrow[j] = m0 + (DIRECT_W ? row - BN : row);   // token rows (unused for weight rows)
+    }
+    token_rows<MOE, CPB>(p, mrow, qbr, orw, v);
+  }
 #pragma unroll
   for (int j = 0; j < CPW; ++j) {
     const int q = pwave + PW * j;
@@ -951,11 +997,7 @@ __global__ void __launch_bounds__((WM * WN + NP) * 64) tiled16_kernel(G16 p, int
       qoff[j] = (uint32_t)r * (uint32_t)p.ldw;
       qis_w[j] = true;
     } else {
-      const int trow = DIRECT_W ? row - BN : row;
-      int br, orw;
-      bool v;
-      token_row<MOE>(p, m0 + trow, br, orw, v);
-      qoff[j] = (uint32_t)br * (uint32_t)(p.lda * 2);
+      qoff[j] = (uint32_t)qbr[j] * (uint32_t)(p.lda * 2);
       qis_w[j] = false;
     }
     qoff[j] += 16 * ((lane & 7) ^ lds_swz(row + (DIRECT_W ? 0 : BN)));
@@ -1012,10 +1054,21 @@ __global__ void __launch_bounds__((WM * WN + NP) * 64) tiled16_kernel(G16 p, int
   };
   auto decode_piece = [&](uint8_t* st, int j, const WBuf1& b) {
     const float sc = wscale_value<FMT>(p, b.s);
-    const float z = ZP ? (float)((pgrow[j] & 1) ? (b.z >> 4) : (b.z & 15)) : 8.0f;
+    const uint32_t zi = ZP ? ((pgrow[j] & 1) ? (b.z >> 4) : (b.z & 15)) : 8u;
+    const float z = (float)zi;
     uint32_t v[PV / 2];
     constexpr int PAIRS_PER_DWORD = 32 / BITS / 2;
-    if constexpr (FMT == kWMxfp4 && !F16) {
+    if constexpr (FMT == kWInt4Zp || FMT == kWInt4Sym) {
+      if (__builtin_fabsf(sc) <= 0x1p123f) {
+        const uint32_t zb = (16u - zi) * 0x01010101u;
+        const float c = -16.0f * sc;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) int4_dword_fma<F16>(b.w[i], zb, sc, c, &v[4 * i]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) decode_dword<FMT, F16>(b.w[i], sc, z, &v[i * PAIRS_PER_DWORD]);
+      }
+    } else if constexpr (FMT == kWMxfp4 && !F16) {
       if (scale_kind<FMT>(p) == kSE8m0 && mxfp4_cvt_ok(b.s)) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) mxfp4_dword_cvt(b.w[i], b.s, &v[4 * i]);
@@ -1235,9 +1288,16 @@ __global__ void __launch_bounds__((WM * WN + NP) * 64) tiled16_kernel(G16 p, int
   wait_vmem();
   if (!is_cons) return;
 
+  EpiRow elate[PRE ? 1 : MT];   // rows not loaded before the loop, as one batch here
+  if constexpr (!PRE) {
+    int mrow[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) mrow[t] = m0 + wm * TM + 16 * t + r16;
+    epi_rows<MOE, MT>(p, mrow, elate);
+  }
 #pragma unroll
   for (int t = 0; t < MT; ++t) {
-    const EpiRow e = PRE ? erow[PRE ? t : 0] : epi_row<MOE>(p, m0 + wm * TM + 16 * t + r16);
+    const EpiRow e = PRE ? erow[PRE ? t : 0] : elate[PRE ? 0 : t];
     const int orw = e.orow;
     if (!e.valid) continue;
 #pragma unroll
@@ -1511,7 +1571,7 @@ int run_moe16(const char* op, const MoeArgs& m, G16 p, void* stream) {
                 "%s: an operand spans more than 4 GiB (the kernels use 32-bit row offsets); split the call", op);
   int rc = check_scale_kind(op, p.ws_kind);
   if (rc) return rc;
-  if (m.num_blocks == 0 || m.num_slots == 0 || m.N == 0) return STRIX_OK;
+  if (m.num_blocks == 0 || m.sorted_len == 0 || m.num_slots == 0 || m.N == 0) return STRIX_OK;
   STRIX_ARCH_GATE();
   p.a = static_cast<const uint16_t*>(m.a); p.lda = m.lda;
   p.out = m.c; p.ldo = m.ldc; p.out_f16 = m.c_dtype == STRIX_F16;

@@ -153,9 +153,14 @@ __global__ void __launch_bounds__(256) stream8_kernel(G8 p) {
   bool bval[MT];
   const uint8_t* ap[MT];
   const float* sap[MT];
+  {
+    int mrow[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) mrow[t] = m0 + 16 * t + r16;
+    token_rows<MOE, MT>(p, mrow, brow, orow, bval);
+  }
 #pragma unroll
   for (int t = 0; t < MT; ++t) {
-    token_row<MOE>(p, m0 + 16 * t + r16, brow[t], orow[t], bval[t]);
     ap[t] = p.a + (int64_t)brow[t] * p.lda + 16 * g4;
     sap[t] = p.sa + (int64_t)brow[t] * p.sa_rs;
   }
@@ -436,13 +441,14 @@ __global__ void __launch_bounds__(64 * NW * KS) ring8_kernel(G8 p) {
   const int e0 = NW == 1 ? 0 : wave;
   const int ne = NW == 1 ? EX : (wave < EX ? 1 : 0);
   const uint8_t* tsrc[TQ];
+  {
+    int mrow[TQ], br[TQ], orw[TQ];
+    bool v[TQ];
 #pragma unroll
-  for (int e = 0; e < TQ; ++e) {
-    const int row = 8 * e + crow;
-    int br, orw;
-    bool v;
-    token_row<MOE>(p, m0 + row, br, orw, v);
-    tsrc[e] = p.a + (int64_t)br * p.lda + 16 * ((lane & 7) ^ lds_swz(row));
+    for (int e = 0; e < TQ; ++e) mrow[e] = m0 + 8 * e + crow;
+    token_rows<MOE, TQ>(p, mrow, br, orw, v);
+#pragma unroll
+    for (int e = 0; e < TQ; ++e) tsrc[e] = p.a + (int64_t)br[e] * p.lda + 16 * ((lane & 7) ^ lds_swz(8 * e + crow));
   }
   // Scale copy: lanes 0..SAL-1 the token rows' activation scales, lanes
   // SAL.. the weight scales (fp8: one per subtile of the block; int8 group:
@@ -593,11 +599,18 @@ __global__ void __launch_bounds__(64 * NW * KS) ring8_kernel(G8 p) {
   }
 
   if (nout0 >= p.n_out) return;
+  int ebrow[MT], eorow[MT];
+  bool ebval[MT];
+  {
+    int mrow[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) mrow[t] = m0 + 16 * t + r16;
+    token_rows<MOE, MT>(p, mrow, ebrow, eorow, ebval);
+  }
 #pragma unroll
   for (int t = 0; t < MT; ++t) {
-    int brow, orow;
-    bool bval;
-    token_row<MOE>(p, m0 + 16 * t + r16, brow, orow, bval);
+    const int brow = ebrow[t], orow = eorow[t];
+    const bool bval = ebval[t];
 #pragma unroll
     for (int so = 0; so < NTH; ++so) {
       float g[4], u[4];
@@ -711,22 +724,19 @@ __global__ void __launch_bounds__(WM * WN * 64) tiled8_kernel(G8 p, int tiles_m,
   // MoE: a wave whose TM token rows are all padding (in an expert's last,
   // partly filled row tile) skips its fragment reads, MFMAs and folds; it
   // still issues its copies and takes every barrier.
+  // The epilogue rows (MoE), loaded before the K loop (dense rows are
+  // arithmetic), cover the wave's TM rows and so also decide this.
   bool rows_live = true;
-  if constexpr (MOE) {
-    bool any = false;
-    for (int r = lane; r < TM; r += 64) {
-      int br, orw;
-      bool v;
-      token_row<true>(p, m0 + wm * TM + r, br, orw, v);
-      any = any || v;
-    }
-    rows_live = __ballot(any) != 0;
-  }
-  // MoE epilogue rows, loaded before the K loop (dense rows are arithmetic).
   EpiRow erow[MOE ? MT : 1];
   if constexpr (MOE) {
+    int mrow[MT];
 #pragma unroll
-    for (int t = 0; t < MT; ++t) erow[t] = epi_row<MOE>(p, m0 + wm * TM + 16 * t + r16);
+    for (int t = 0; t < MT; ++t) mrow[t] = m0 + wm * TM + 16 * t + r16;
+    epi_rows<MOE, MT>(p, mrow, erow);
+    bool any = false;
+#pragma unroll
+    for (int t = 0; t < MT; ++t) any = any || erow[t].valid;
+    rows_live = __ballot(any) != 0;
   }
   auto wrow_of = [&](int j) -> int {  // first weight row of LDS weight subtile j
     if constexpr (GATED) {
@@ -743,6 +753,14 @@ __global__ void __launch_bounds__(WM * WN * 64) tiled8_kernel(G8 p, int tiles_m,
   // chunk (l%8) ^ swz(row) of that row.
   uint32_t qoff[QPW];
   bool qis_w[QPW];
+  int qbr[QPW];   // activation rows of the token copies (one batch of lookups)
+  {
+    int mrow[QPW], orw[QPW];
+    bool v[QPW];
+#pragma unroll
+    for (int j = 0; j < QPW; ++j) mrow[j] = m0 + 8 * (wave + W * j - WCOPIES) + (lane >> 3);
+    token_rows<MOE, QPW>(p, mrow, qbr, orw, v);
+  }
 #pragma unroll
   for (int j = 0; j < QPW; ++j) {
     const int q = wave + W * j;           // wave-uniform (a copy holds weight rows only
@@ -758,10 +776,7 @@ __global__ void __launch_bounds__(WM * WN * 64) tiled8_kernel(G8 p, int tiles_m,
       off = (uint32_t)r * (uint32_t)p.ldw + 16 * ((lane & 7) ^ lds_swz(row));
     } else {
       const int trow = 8 * (q - WCOPIES) + (lane >> 3);  // token row of the block
-      int br, orw;
-      bool v;
-      token_row<MOE>(p, m0 + trow, br, orw, v);
-      off = (uint32_t)br * (uint32_t)p.lda + 16 * ((lane & 7) ^ lds_swz(trow));
+      off = (uint32_t)qbr[j] * (uint32_t)p.lda + 16 * ((lane & 7) ^ lds_swz(trow));
     }
     qis_w[j] = is_w;
     qoff[j] = off;
@@ -1541,7 +1556,7 @@ int strix_moe_gemm_w4a8(void* c, int64_t ldc, int c_dtype, const int8_t* qa, int
   const int64_t half_tile = block_m == 256 ? 128 : 64;
   STRIX_REQUIRE(!silu_mul || (N / 2) % half_tile == 0, "%s: gated N/2 must be a multiple of %lld at block_m %lld",
                 op, (long long)half_tile, (long long)block_m);
-  if (num_blocks == 0 || num_slots == 0 || N == 0) return STRIX_OK;
+  if (num_blocks == 0 || sorted_len == 0 || num_slots == 0 || N == 0) return STRIX_OK;
   STRIX_ARCH_GATE();
   G8 p = {};
   p.w = w4; p.ldw = ldw; p.w_es = w_es; p.w_kbs = 64;
@@ -1585,7 +1600,7 @@ int moe_gemm_fp8(const char* op, void* c, int64_t ldc, int c_dtype, const uint8_
   STRIX_REQUIRE(ldc >= n_out && ldc % 4 == 0 && aligned(c, 8), "%s: output rows must be >= %lld, 8-byte aligned",
                 op, (long long)n_out);
   STRIX_REQUIRE(!silu_mul || (N / 2) % 128 == 0, "%s: gated FP8-block N/2 must be a multiple of 128", op);
-  if (num_blocks == 0 || num_slots == 0 || N == 0) return STRIX_OK;
+  if (num_blocks == 0 || sorted_len == 0 || num_slots == 0 || N == 0) return STRIX_OK;
   STRIX_ARCH_GATE();
   G8 p = {};
   p.w = w;

@@ -40,21 +40,56 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
-// Token row of MFMA column m (block-relative index already added): brow is
-// the activation row to read (a valid row even for padding), orow the output
-// row, valid whether the result is stored.
+// Makes x a value the compiler must have in a register here. Applied to
+// loaded values after all loads of a batch are issued, it keeps the compiler
+// from turning a select of a loaded value into a branch around the load
+// (which it does otherwise, with a wait right after each such load).
+template <class T>
+__device__ __forceinline__ T settle(T x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
+// Token rows of MFMA columns m[i] (block-relative index already added):
+// brow is the activation row to read (a valid row even for padding), orow
+// the output row, valid whether the result is stored. The MoE lookups of a
+// batch go out together, without branches (an index past sorted_ids reads
+// entry 0 and is then discarded; the launchers return before any kernel when
+// sorted_ids is empty): one memory round trip for the batch.
+template <bool MOE, int N, class P>
+__device__ __forceinline__ void token_rows(const P& p, const int (&m)[N], int (&brow)[N], int (&orow)[N],
+                                           bool (&valid)[N]) {
+  if constexpr (MOE) {
+    int raw[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) raw[i] = p.sorted_ids[(m[i] >= 0 && m[i] < p.sorted_len) ? m[i] : 0];
+#pragma unroll
+    for (int i = 0; i < N; ++i) raw[i] = settle(raw[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int sid = (m[i] >= 0 && m[i] < p.sorted_len) ? raw[i] : p.num_slots;
+      valid[i] = sid >= 0 && sid < p.num_slots;
+      brow[i] = valid[i] ? (int)((uint32_t)sid / (uint32_t)max(p.top_k, 1)) : 0;
+      orow[i] = sid;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      valid[i] = m[i] >= 0 && m[i] < p.M;
+      brow[i] = valid[i] ? m[i] : 0;
+      orow[i] = m[i];
+    }
+  }
+}
 template <bool MOE, class P>
 __device__ __forceinline__ void token_row(const P& p, int m, int& brow, int& orow, bool& valid) {
-  if constexpr (MOE) {
-    const int sid = (m >= 0 && m < p.sorted_len) ? p.sorted_ids[m] : p.num_slots;
-    valid = sid >= 0 && sid < p.num_slots;
-    brow = valid ? sid / p.top_k : 0;
-    orow = sid;
-  } else {
-    valid = m >= 0 && m < p.M;
-    brow = valid ? m : 0;
-    orow = m;
-  }
+  const int mm[1] = {m};
+  int br[1], orw[1];
+  bool v[1];
+  token_rows<MOE, 1>(p, mm, br, orw, v);
+  brow = br[0];
+  orow = orw[0];
+  valid = v[0];
 }
 
 // Stores four consecutive output columns col0..col0+3 of row orow.
@@ -126,17 +161,38 @@ struct EpiRow {
   int valid;
   float tw;
 };
+// Epilogue rows of MFMA columns m[i]: the row lookups, then the top-k
+// weights (one more round trip), each as one batch.
+template <bool MOE, int N, class P>
+__device__ __forceinline__ void epi_rows(const P& p, const int (&m)[N], EpiRow (&e)[N]) {
+  int br[N], orw[N];
+  bool v[N];
+  token_rows<MOE, N>(p, m, br, orw, v);
+  float w[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) w[i] = 1.f;
+  if constexpr (MOE) {
+    if (p.topk_w) {   // uniform; the loads are unconditional (slot 0 for padding rows)
+#pragma unroll
+      for (int i = 0; i < N; ++i) w[i] = p.topk_w[v[i] ? orw[i] : 0];
+#pragma unroll
+      for (int i = 0; i < N; ++i) w[i] = settle(w[i]);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    e[i].brow = br[i];
+    e[i].orow = orw[i];
+    e[i].valid = v[i];
+    e[i].tw = v[i] ? w[i] : 1.f;
+  }
+}
 template <bool MOE, class P>
 __device__ __forceinline__ EpiRow epi_row(const P& p, int m) {
-  EpiRow e;
-  bool v;
-  token_row<MOE>(p, m, e.brow, e.orow, v);
-  e.valid = v;
-  e.tw = 1.f;
-  if constexpr (MOE) {
-    if (p.topk_w && v) e.tw = p.topk_w[e.orow];
-  }
-  return e;
+  const int mm[1] = {m};
+  EpiRow e[1];
+  epi_rows<MOE, 1>(p, mm, e);
+  return e[0];
 }
 
 // The hardware deals the blocks of a launch to the eight XCDs round robin

@@ -238,3 +238,21 @@ def test_moe_gemm_w4a8_rejects_unsupported_tiles():
     c = torch.empty(4, n, dtype=torch.bfloat16, device=DEV)
     with pytest.raises(RuntimeError, match="unsupported block_m/block_n"):
         S.moe_gemm_w4a8(c, qa, sa, w, s, sorted_ids, expert_ids, num_post, None, 1, 128, 256, False, "silu")
+
+
+def test_moe_gemm_w4a8_empty_sorted_ids_writes_nothing():
+    """sorted_ids empty (no routed positions): the call returns before any
+    kernel and leaves the output as it was."""
+    e, top_k, t, n, k = 8, 4, 3, 256, 256
+    q, scales, _, ids, weights = _moe_case(e, t, top_k, n, k, 5, torch.bfloat16)
+    a = torch.randn(t * top_k, k, generator=_g(5)).to(torch.bfloat16)
+    qa, sa = _quant(a)
+    c = torch.full((t * top_k, n), 7.0, dtype=torch.bfloat16, device=DEV)
+    sorted_ids = torch.empty(0, dtype=torch.int32, device=DEV)
+    expert_ids = torch.zeros(1, dtype=torch.int32, device=DEV)
+    num_post = torch.zeros(1, dtype=torch.int32, device=DEV)
+    for block_m, block_n in ((64, 128), (256, 256)):
+        S.moe_gemm_w4a8(c, qa, sa, pack_low_first(q).to(DEV), scales.to(DEV), sorted_ids, expert_ids, num_post,
+                        weights.reshape(-1).to(DEV), 1, block_m, block_n, False, "silu")
+    torch.cuda.synchronize()
+    assert bool((c == 7.0).all())

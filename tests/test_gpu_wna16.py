@@ -137,3 +137,22 @@ def test_config5_fused_moe(t, c5_weights):
                            lambda e: oracle.wna16_zp_decode(d["w2"][e], d["w2_s"][e], d["w2_z"][e], 128))
     assert ref.shape == out.shape
     assert peak_rel_err(out, ref) <= TOL
+
+
+def test_empty_sorted_ids_writes_nothing(zp_experts):
+    """No routed positions at all (sorted_ids empty, one expert block): the
+    call returns without touching the output (the kernels' row lookups
+    assume a non-empty sorted_ids, so the launcher stops first)."""
+    d = zp_experts
+    w, s, z = d["w13"], d["w13_s"], d["w13_z"]
+    n, k = w.size(1), w.size(2) * 8
+    a = torch.randn(3, k).to(torch.bfloat16).to(DEV)
+    c = torch.full((3 * TOPK, n // 2), 7.0, dtype=torch.bfloat16, device=DEV)
+    sorted_ids = torch.empty(0, dtype=torch.int32, device=DEV)
+    expert_ids = torch.zeros(1, dtype=torch.int32, device=DEV)
+    num_post = torch.zeros(1, dtype=torch.int32, device=DEV)
+    for block_m in (16, 256):
+        torch.ops.strix.moe_gemm_w4a16_zp(c, a, w.to(DEV), s.to(DEV), z.to(DEV), sorted_ids, expert_ids, num_post,
+                                          None, TOPK, block_m, 64, True, "silu", 128)
+    torch.cuda.synchronize()
+    assert bool((c == 7.0).all())
