@@ -109,6 +109,8 @@ WORKLOADS = {
                      lambda: _fp8_decode(1, True), _dense_bytes(1)),
     "c2_m16_kmajor": ("config-2 FP8-block GEMM, M=16 (K-block-major weights)", lambda: _fp8_decode(16, True),
                       _dense_bytes(16)),
+    "c2_m256_kmajor": ("config-2 FP8-block GEMM, M=256 (K-block-major weights)", lambda: _fp8_decode(256, True),
+                       _dense_bytes(256)),
     "c1_m32": ("config-1 int8 W8A8 GEMM, M=32 N=K=5120", _int8_decode,
                5120 * 5120 + 5120 * 4 + 32 * 5120 + 32 * 4 + 32 * 5120 * 2),
     "c3_t1": ("config-3 FP8-block MoE, T=1", lambda: _moe("c3", 1), None),
