@@ -112,7 +112,10 @@ int strix_w8a8_int8_group_gemm(const int8_t* qa, int64_t lda, const float* sa, i
  * sibling of moe_gemm_fp8, csrc/torch_ops.cpp:225-228,
  * csrc/moe/moe_gemm_w8a16.hip:444-579). Rows of qa are tokens (slot / top_k);
  * silu_mul fuses act(gate)*up ([gate; up] weight rows, c gets N/2 columns);
- * topk_weights (may be NULL) scales each output row. */
+ * topk_weights (may be NULL) scales each output row. With sorted_len,
+ * num_blocks or num_slots 0 the call returns STRIX_OK without launching
+ * (nothing is routed, c is left as it is); the same holds for every MoE GEMM
+ * below. */
 int strix_moe_gemm_fp8_w8a8(void* c, int64_t ldc, int c_dtype, const uint8_t* qa, int64_t lda,
                             const float* sa, int64_t sa_ld, const uint8_t* w, int64_t w_es, int64_t ldw,
                             const float* sw, int64_t sw_es, int64_t sw_ns, const int32_t* sorted_ids,
